@@ -1,0 +1,158 @@
+/*
+ * C ABI of the MI355X (gfx950) paged FP8-KV decode-attention library
+ * (libl20_paged_decode_hip.so).
+ *
+ * Every entry point takes plain pointers, sizes and strides; no torch or HIP
+ * types appear in the signatures (a HIP stream is passed as `void *`).  The
+ * torch binding (l20_paged_decode_ops.so, TORCH_LIBRARY(l20_stack)) and the
+ * ctypes binding used by the tests both call through these functions.
+ *
+ * Reference interfaces replaced (paths relative to the reference repo root):
+ *   l20_pd_fp8_e4m3_split_out  <- l20_paged_decode_fp8_e4m3_split_out_cuda
+ *                                 integrations/vllm/cuda/l20_paged_decode.cu:651-725
+ *                                 (declared at l20_paged_decode.cpp:47-60, bound by
+ *                                 TORCH_LIBRARY(l20_stack) at l20_paged_decode.cpp:128-143)
+ *   l20_pd_fp8_e4m3_check      <- the TORCH_CHECK block of the same function,
+ *                                 l20_paged_decode.cu:665-688 (argument validation
+ *                                 without touching the GPU)
+ *   l20_pd_num_splits          <- num_splits = ceil(max_seq_len / split_size),
+ *                                 l20_paged_decode.cu:684
+ *   l20_pd_fp8_e4m3_dequant_f32/_bf16
+ *                              <- fp8x2_e4m3fn_to_float2, l20_paged_decode.cu:20-33
+ *                                 (the device-side e4m3fn conversion, exposed as a
+ *                                 bulk dequantiser)
+ */
+#ifndef L20_PAGED_DECODE_H_
+#define L20_PAGED_DECODE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define L20_PD_ABI_VERSION 1
+
+/* Element types for query/output and the partial-output workspace. */
+enum l20_pd_dtype {
+  L20_PD_BF16 = 0,
+  L20_PD_FP16 = 1,
+  L20_PD_FP32 = 2
+};
+
+/* Return codes. */
+enum l20_pd_status {
+  L20_PD_OK = 0,
+  L20_PD_EINVAL = 1,   /* argument validation failed; see l20_pd_last_error() */
+  L20_PD_ELAUNCH = 2   /* a HIP launch or runtime call failed */
+};
+
+/*
+ * Arguments of one paged FP8 decode-attention call.  Strides are in elements
+ * of the tensor's own type (bytes for the fp8 caches).  The last dimension of
+ * every tensor (head_dim) must be contiguous.
+ *
+ *   query          [batch*q_len, num_q_heads, head_dim]   bf16 or fp16
+ *   key/value      [num_pages, page_size=16, num_kv_heads, head_dim]  e4m3fn bytes
+ *   block_table    [batch, >= ceil(max_seq_len/16)]  int32 physical page ids
+ *   seq_lens       [batch]  int32, each <= max_seq_len, includes the q_len new tokens
+ *   partial_output [batch*q_len, num_q_heads, >= num_splits, head_dim]  fp32 or fp16
+ *   partial_max/sum[batch*q_len, num_q_heads, >= num_splits]  fp32
+ *   output         [batch*q_len, num_q_heads, head_dim]  same dtype as query
+ *   lse            [batch*q_len, num_q_heads] fp32 natural-log LSE, or NULL
+ *
+ * Query row b*q_len+i attends to keys 0 .. seq_lens[b]-q_len+i (causal among
+ * the q_len newest tokens; q_len=1 is plain decode).  K/V are dequantised as
+ * code * scale with the per-head scale arrays (fp32 [num_kv_heads], device
+ * memory) when non-NULL, else with the scalar scales.  softmax_scale <= 0
+ * selects head_dim^-0.5.  The contents of the partial workspace after a call
+ * are unspecified.
+ */
+typedef struct l20_pd_fp8_args {
+  const void *query;
+  int32_t query_dtype;
+  int64_t q_stride_row, q_stride_head;
+
+  const uint8_t *key_cache;
+  int64_t k_stride_page, k_stride_token, k_stride_head;
+  const uint8_t *value_cache;
+  int64_t v_stride_page, v_stride_token, v_stride_head;
+  int64_t num_pages;
+  int32_t page_size;
+
+  const int32_t *block_table;
+  int64_t bt_stride_row;
+  int32_t bt_max_pages;
+  const int32_t *seq_lens;
+
+  void *partial_output;
+  int32_t partial_dtype;
+  int64_t po_stride_row, po_stride_head, po_stride_split;
+  int32_t partial_splits;
+  float *partial_max;
+  int64_t pm_stride_row, pm_stride_head, pm_stride_split;
+  float *partial_sum;
+  int64_t ps_stride_row, ps_stride_head, ps_stride_split;
+
+  void *output;
+  int64_t o_stride_row, o_stride_head;
+  float *lse;
+  int64_t lse_stride_row, lse_stride_head;
+
+  float k_scale, v_scale;
+  const float *k_scale_per_head;
+  const float *v_scale_per_head;
+  float softmax_scale;
+
+  int32_t batch, q_len, num_q_heads, num_kv_heads, head_dim;
+  int32_t max_seq_len, split_size;
+} l20_pd_fp8_args;
+
+/* ABI version of the loaded library (L20_PD_ABI_VERSION). */
+int32_t l20_pd_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *l20_pd_last_error(void);
+
+/* ceil(max_seq_len / split_size); 0 for max_seq_len <= 0. */
+int32_t l20_pd_num_splits(int32_t max_seq_len, int32_t split_size);
+
+/* Validate `args` exactly as l20_pd_fp8_e4m3_split_out does, without any
+ * HIP call.  Returns L20_PD_OK or L20_PD_EINVAL. */
+int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args);
+
+/* Enqueue the split-KV partial kernel and the LSE merge kernel on `stream`
+ * (hipStream_t, NULL = default stream).  Asynchronous; allocates nothing. */
+int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
+
+/* The two stages of l20_pd_fp8_e4m3_split_out, enqueued separately (same
+ * arguments, same validation): the split-KV partial kernel
+ * (<- paged_decode_fp8_e4m3_partial_kernel, l20_paged_decode.cu:291-422,
+ * launched at :692-712) and the LSE merge kernel (<- paged_decode_merge_kernel,
+ * l20_paged_decode.cu:424-463, launched at :713-723).  split_out is exactly
+ * partial followed by merge; the merge is a no-op when ceil(max_seq_len /
+ * split_size) <= 1. */
+int32_t l20_pd_fp8_e4m3_partial(const l20_pd_fp8_args *args, void *stream);
+int32_t l20_pd_fp8_e4m3_merge(const l20_pd_fp8_args *args, void *stream);
+
+/* Split size the library picks for a call shape when the caller has no
+ * preference: a multiple of 16 in [64, 1024] that gives enough
+ * (sequence, kv head, split) work items for `cu_count` compute units. */
+int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads,
+                                  int32_t max_seq_len, int32_t cu_count);
+
+/* Bulk e4m3fn dequantisation on the GPU: dst[i] = float(src[i]) * scale.
+ * Uses the same conversion instruction as the attention kernel's V path. */
+int32_t l20_pd_fp8_e4m3_dequant_f32(const uint8_t *src, float *dst, int64_t n,
+                                    float scale, void *stream);
+
+/* Bulk e4m3fn -> bf16 (raw uint16 bits) with the attention kernel's K path. */
+int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst,
+                                     int64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* L20_PAGED_DECODE_H_ */

@@ -1,0 +1,872 @@
+// Paged FP8 (OCP e4m3fn) KV-cache decode attention for MI355X (gfx950).
+//
+// Two kernels per call, both enqueued on the caller's stream:
+//
+//  pd_fp8_partial<QT, D, NQT>   grid (num_splits, num_kv_heads, batch), 1-4 waves.
+//    One workgroup owns one (sequence, KV head, split) work item and computes
+//    attention for ALL query rows of that KV head (GQA group x q_len, padded to
+//    16 * NQT MFMA columns), so each K/V page is read from HBM exactly once.
+//    The split's 16-token pages are dealt to the waves in 32-token blocks.
+//    Per block and lane:
+//      K: 2 tiles x D/64 x 16 B loads (token = lane%16, 64-byte half-rows),
+//         fp8 -> bf16/f16 conversion (exact), S^T = K . Q^T on
+//         v_mfma_f32_16x16x32_{bf16,f16}: rows = tokens, columns = query rows.
+//      softmax: each lane holds 8 scores of one query column; the block max is
+//         reduced across the four 16-lane groups; exp2 with the K scale, the
+//         softmax scale and log2(e) folded into one multiplier.
+//      V: 8 tokens x D/16 contiguous bytes per lane; the fp8 -> f32 -> f16
+//         conversion packs token pairs, which transposes V for the MFMA A
+//         operand in registers (no LDS pass).  O^T += V^T . P^T with P in f16.
+//    The waves' (m, l, O) are combined through LDS.  A sequence with a single
+//    split writes the final output and LSE; otherwise the fp32 partial
+//    (O / l, m, l) goes to the caller's workspace.
+//
+//  pd_merge<QT, D>   grid (num_q_heads, batch*q_len), 256 threads.
+//    LSE merge of a row's splits: M = max m_s, w_s = 2^(m_s - M) l_s,
+//    out = sum w_s o_s / sum w_s, lse = ln2 (M + log2 sum w_s).
+//
+// Reference semantics (paths relative to the reference repo root):
+//   integrations/vllm/cuda/l20_paged_decode.cu:291-422 (partial),
+//   :424-463 (merge), :651-725 (host launcher and argument checks);
+//   scripts/smoke_cuda_paged_fp8_decode_op.py:22-41 (dequantise-then-attend).
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "l20_paged_decode.h"
+
+namespace l20pd {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kPage = 16;
+constexpr int kMaxWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct PartialParams {
+  const void *q;
+  int64_t q_srow, q_shead;
+  const uint8_t *k;
+  int64_t k_spage, k_stok, k_shead;
+  const uint8_t *v;
+  int64_t v_spage, v_stok, v_shead;
+  const int32_t *bt;
+  int64_t bt_srow;
+  const int32_t *seq_lens;
+  int64_t num_pages;
+  void *po;
+  int64_t po_srow, po_shead, po_ssplit;
+  float *pm;
+  int64_t pm_srow, pm_shead, pm_ssplit;
+  float *pl;
+  int64_t pl_srow, pl_shead, pl_ssplit;
+  void *out;
+  int64_t o_srow, o_shead;
+  float *lse;
+  int64_t lse_srow, lse_shead;
+  float k_scale, v_scale;
+  const float *k_scale_ph;
+  const float *v_scale_ph;
+  float qk_scale_log2;  // softmax_scale * log2(e)
+  int q_len, num_q_heads, num_kv_heads, group, split_size, num_splits;
+  int po_f32;
+  int l_cap;  // min(num_splits * split_size, block-table pages * 16): tokens past it are never touched
+};
+
+// ---------------------------------------------------------------------------
+// Element helpers
+// ---------------------------------------------------------------------------
+template <typename QT> struct MfmaTypes;
+template <> struct MfmaTypes<__bf16> { typedef bf16x8 vec8; };
+template <> struct MfmaTypes<_Float16> { typedef f16x8 vec8; };
+
+// Four e4m3fn codes (one dword) -> four bf16 (exact: every e4m3fn value is a
+// bf16 value).  gfx950 v_cvt_scalef32_pk_bf16_fp8 with scale 1.0.
+__device__ __forceinline__ void fp8x4_to(bf16x8 &dst, int slot, int w) {
+  bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  dst[slot + 0] = lo[0];
+  dst[slot + 1] = lo[1];
+  dst[slot + 2] = hi[0];
+  dst[slot + 3] = hi[1];
+}
+__device__ __forceinline__ void fp8x4_to(f16x8 &dst, int slot, int w) {
+  f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+  f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+  dst[slot + 0] = lo[0];
+  dst[slot + 1] = lo[1];
+  dst[slot + 2] = hi[0];
+  dst[slot + 3] = hi[1];
+}
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Byte pair (sel=0: bytes 0,1; sel=1: bytes 2,3) of a dword -> two f32.
+__device__ __forceinline__ f32x2 fp8x2_f32(int w, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+}
+
+template <typename QT> __device__ __forceinline__ QT from_f32(float x);
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+
+__device__ __forceinline__ float wave_max_xor16_32(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_xor16_32(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+// Raw fp8 bytes of one 32-token block (two 16-token pages) held by one lane.
+template <int D> struct BlockRaw;
+template <> struct BlockRaw<128> {
+  i32x4 k[2][2];  // [tile][half-row chunk]: 16 B at d = 64*c + 16*(lane/16)
+  i32x2 v[8];     // [token slot]: 8 B at d = 8*(lane%16)
+};
+template <> struct BlockRaw<64> {
+  i32x4 k[2][1];
+  int v[8];       // 4 B at d = 4*(lane%16)
+};
+
+// ---------------------------------------------------------------------------
+// Partial kernel
+// ---------------------------------------------------------------------------
+template <typename QT, int D, int NQT>
+__global__ __launch_bounds__(256) void pd_fp8_partial(PartialParams p) {
+  typedef typename MfmaTypes<QT>::vec8 qvec8;
+  constexpr int NCH = D / 64;        // 64-byte K chunks per token row
+  constexpr int NS = 2 * NCH;        // 32-wide k slices of the QK product
+  constexpr int NT = D / 16;         // 16-row d tiles of the PV product
+  constexpr int DPL = D / 4;         // contiguous output dims per lane
+  constexpr int LDS_STRIDE = D + 4;  // padded row of the LDS combine buffer
+
+  __shared__ float sm_o[kMaxWaves][16][LDS_STRIDE];
+  __shared__ float sm_m[kMaxWaves][16];
+  __shared__ float sm_l[kMaxWaves][16];
+
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int L = min(p.seq_lens[b], p.l_cap);
+  const int split_start = split * p.split_size;
+  if (split_start >= L) {  // uniform: nothing in this split
+    if (split == 0) {
+      // Empty sequence: zero output and -inf LSE for all its query rows.
+      const int rows = p.group * p.q_len;
+      for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
+        const int col = idx / D;
+        const int d = idx - col * D;
+        const int g = col / p.q_len;
+        const int i = col - g * p.q_len;
+        const int64_t row = (int64_t)b * p.q_len + i;
+        const int64_t h = (int64_t)kvh * p.group + g;
+        reinterpret_cast<QT *>(p.out)[row * p.o_srow + h * p.o_shead + d] = from_f32<QT>(0.0f);
+        if (d == 0 && p.lse) p.lse[row * p.lse_srow + h * p.lse_shead] = -INFINITY;
+      }
+    }
+    return;
+  }
+  const int n_splits_b = (L + p.split_size - 1) / p.split_size;
+  const int split_end = min(split_start + p.split_size, L);
+  const bool direct = (n_splits_b == 1);
+
+  const int nwaves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+  const int q_len = p.q_len;
+  const int mcols = p.group * q_len;
+
+  const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
+  const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
+  const float c_log2 = k_scale * p.qk_scale_log2;
+
+  // ---- query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16 ----
+  qvec8 qop[NQT][NS];
+  int lim[NQT];  // last visible token for this lane's column
+#pragma unroll
+  for (int qt = 0; qt < NQT; ++qt) {
+    const int col = 16 * qt + n16;
+    const int g = col / q_len;
+    const int i = col - g * q_len;
+    lim[qt] = min(split_end - 1, L - q_len + i);
+    if (col < mcols) {
+      const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
+                       (int64_t)(kvh * p.group + g) * p.q_shead;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
+        qop[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) qop[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
+    }
+  }
+  int min_lim = min(split_end - 1, L - q_len);
+
+  // ---- page ids of this wave's blocks: lane e -> (block e/2, tile e%2) ----
+  const int tiles = (split_end - split_start + kPage - 1) / kPage;
+  const int nblk = (tiles + 1) >> 1;
+  int pid = -1;
+  {
+    const int ti = 2 * (wave + nwaves * (lane >> 1)) + (lane & 1);
+    if (ti < tiles) {
+      const int v = p.bt[(int64_t)b * p.bt_srow + split_start / kPage + ti];
+      pid = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
+    }
+  }
+
+  const int64_t koff = (int64_t)n16 * p.k_stok + (int64_t)kvh * p.k_shead + 16 * j;
+  const int64_t voff = (int64_t)(4 * j) * p.v_stok + (int64_t)kvh * p.v_shead + (D / 16) * n16;
+
+  f32x4 acc[NQT][NT];
+  float m_run[NQT], l_run[NQT];
+#pragma unroll
+  for (int qt = 0; qt < NQT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  auto load_block = [&](BlockRaw<D> &r, int it) {
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      const int page = __builtin_amdgcn_readlane(pid, 2 * it + T);
+      if (page >= 0) {
+        const uint8_t *kp = p.k + (int64_t)page * p.k_spage + koff;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) r.k[T][c] = *reinterpret_cast<const i32x4 *>(kp + 64 * c);
+        const uint8_t *vp = p.v + (int64_t)page * p.v_spage + voff;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (D == 128)
+            r.v[4 * T + e] = *reinterpret_cast<const i32x2 *>(vp + e * p.v_stok);
+          else
+            r.v[4 * T + e] = *reinterpret_cast<const int *>(vp + e * p.v_stok);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) r.k[T][c] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (D == 128)
+            r.v[4 * T + e] = i32x2{0, 0};
+          else
+            r.v[4 * T + e] = 0;
+        }
+      }
+    }
+  };
+
+  auto compute_block = [&](BlockRaw<D> &r, int blk) {
+    const int tok0 = split_start + 32 * blk;
+    // Tokens past the end of the sequence may hold arbitrary bytes (NaN
+    // codes included): zero their V so that p = 0 contributes exactly 0.
+    if (tok0 + 32 > L) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+        if (t >= L) {
+          if constexpr (D == 128)
+            r.v[e] = i32x2{0, 0};
+          else
+            r.v[e] = 0;
+        }
+      }
+    }
+    // ---- S^T = K . Q^T ----
+    f32x4 sc[NQT][2];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const i32x4 raw = r.k[T][s >> 1];
+        qvec8 kop;
+        fp8x4_to(kop, 0, raw[2 * (s & 1)]);
+        fp8x4_to(kop, 4, raw[2 * (s & 1) + 1]);
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
+      }
+    }
+    // ---- online softmax (log2 domain) ----
+    const bool need_mask = (tok0 + 31 > min_lim);
+    f16x8 pop[NQT];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = sc[qt][e >> 2][e & 3] * c_log2;
+      if (need_mask) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+          x[e] = (t <= lim[qt]) ? x[e] : -INFINITY;
+        }
+      }
+      float mloc = x[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
+      mloc = wave_max_xor16_32(mloc);
+      const float m_new = fmaxf(m_run[qt], mloc);
+      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
+      float psum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(x[e] - m_use);
+        const float p1 = __builtin_amdgcn_exp2f(x[e + 1] - m_use);
+        psum += p0 + p1;
+        const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+        pop[qt][e] = h[0];
+        pop[qt][e + 1] = h[1];
+      }
+      l_run[qt] = l_run[qt] * alpha + psum;
+      m_run[qt] = m_new;
+      if (__any(alpha != 1.0f)) {  // wave-uniform skip once the maxima settle
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[qt][t] *= alpha;
+      }
+    }
+    // ---- O^T += V^T . P^T ----
+#pragma unroll
+    for (int tp = 0; tp < NT; tp += 2) {
+      // d tiles tp, tp+1 use byte pair (tp % 4, tp % 4 + 1) of dword tp / 4
+      f16x8 va, vb;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        int w0, w1;
+        if constexpr (D == 128) {
+          w0 = r.v[e][tp >> 2];
+          w1 = r.v[e + 1][tp >> 2];
+        } else {
+          w0 = r.v[e];
+          w1 = r.v[e + 1];
+        }
+        const f32x2 f0 = fp8x2_f32(w0, (tp & 3) != 0);
+        const f32x2 f1 = fp8x2_f32(w1, (tp & 3) != 0);
+        const f16x2 ha = __builtin_convertvector(f32x2{f0[0], f1[0]}, f16x2);
+        const f16x2 hb = __builtin_convertvector(f32x2{f0[1], f1[1]}, f16x2);
+        va[e] = ha[0];
+        va[e + 1] = ha[1];
+        vb[e] = hb[0];
+        vb[e + 1] = hb[1];
+      }
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        acc[qt][tp] = mfma16(va, pop[qt], acc[qt][tp]);
+        acc[qt][tp + 1] = mfma16(vb, pop[qt], acc[qt][tp + 1]);
+      }
+    }
+  };
+
+  // ---- main loop: this wave's blocks blk = wave, wave + nwaves, ... ----
+  {
+    BlockRaw<D> cur, nxt;
+    int it = 0;
+    int blk = wave;
+    if (blk < nblk) load_block(cur, 0);
+    for (; blk < nblk; blk += nwaves, ++it) {
+      if (blk + nwaves < nblk) load_block(nxt, it + 1);
+      compute_block(cur, blk);
+      cur = nxt;
+    }
+  }
+
+  // ---- combine the waves through LDS, one 16-column query tile at a time ----
+  constexpr int D4 = D / 4;
+#pragma unroll
+  for (int qt = 0; qt < NQT; ++qt) {
+    const float l_tot = wave_sum_xor16_32(l_run[qt]);
+    if (qt > 0) __syncthreads();  // previous tile's readers are done
+    if (j == 0) {
+      sm_m[wave][n16] = m_run[qt];
+      sm_l[wave][n16] = l_tot;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) sm_o[wave][n16][DPL * j + rr * NT + t] = acc[qt][t][rr];
+    }
+    __syncthreads();
+    const int tile_cols = min(16, mcols - 16 * qt);
+    const int total = tile_cols * D4;
+    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+      const int c16 = idx / D4;
+      const int d = 4 * (idx - c16 * D4);
+      float mm = -INFINITY;
+      for (int w = 0; w < nwaves; ++w) mm = fmaxf(mm, sm_m[w][c16]);
+      const float msafe = (mm == -INFINITY) ? 0.0f : mm;
+      float lsum = 0.0f;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < nwaves; ++w) {
+        const float wt = __builtin_amdgcn_exp2f(sm_m[w][c16] - msafe);
+        lsum += wt * sm_l[w][c16];
+        o += wt * *reinterpret_cast<const f32x4 *>(&sm_o[w][c16][d]);
+      }
+      const float inv = (lsum > 0.0f) ? v_scale / lsum : 0.0f;
+      o *= inv;
+      const int col = 16 * qt + c16;
+      const int g = col / q_len;
+      const int i = col - g * q_len;
+      const int64_t row = (int64_t)b * q_len + i;
+      const int64_t h = (int64_t)kvh * p.group + g;
+      if (direct) {
+        QT *dst = reinterpret_cast<QT *>(p.out) + row * p.o_srow + h * p.o_shead + d;
+        dst[0] = from_f32<QT>(o[0]);
+        dst[1] = from_f32<QT>(o[1]);
+        dst[2] = from_f32<QT>(o[2]);
+        dst[3] = from_f32<QT>(o[3]);
+        if (d == 0 && p.lse) {
+          // v_log_f32 is log2
+          p.lse[row * p.lse_srow + h * p.lse_shead] =
+              (lsum > 0.0f) ? kLn2 * (msafe + __builtin_amdgcn_logf(lsum)) : -INFINITY;
+        }
+      } else {
+        const int64_t po_idx = row * p.po_srow + h * p.po_shead + (int64_t)split * p.po_ssplit + d;
+        if (p.po_f32) {
+          *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.po) + po_idx) = o;
+        } else {
+          _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx;
+          dst[0] = (_Float16)o[0];
+          dst[1] = (_Float16)o[1];
+          dst[2] = (_Float16)o[2];
+          dst[3] = (_Float16)o[3];
+        }
+        if (d == 0) {
+          p.pm[row * p.pm_srow + h * p.pm_shead + (int64_t)split * p.pm_ssplit] = mm;
+          p.pl[row * p.pl_srow + h * p.pl_shead + (int64_t)split * p.pl_ssplit] = lsum;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LSE merge kernel
+// ---------------------------------------------------------------------------
+struct MergeParams {
+  const void *po;
+  int64_t po_srow, po_shead, po_ssplit;
+  const float *pm;
+  int64_t pm_srow, pm_shead, pm_ssplit;
+  const float *pl;
+  int64_t pl_srow, pl_shead, pl_ssplit;
+  const int32_t *seq_lens;
+  void *out;
+  int64_t o_srow, o_shead;
+  float *lse;
+  int64_t lse_srow, lse_shead;
+  int q_len, split_size, num_splits, po_f32;
+  int l_cap;  // same clamp as the partial kernel
+};
+
+template <typename QT, int D>
+__global__ __launch_bounds__(256) void pd_merge(MergeParams p) {
+  constexpr int D4 = D / 4;
+  constexpr int SLOTS = 256 / D4;  // splits processed side by side
+  __shared__ float red[256];
+  __shared__ f32x4 part[SLOTS][D4];
+  __shared__ float wpart[SLOTS];
+
+  const int h = blockIdx.x;
+  const int row = blockIdx.y;
+  const int b = row / p.q_len;
+  const int L = min(p.seq_lens[b], p.l_cap);
+  const int n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
+  if (n <= 1) return;  // the partial kernel wrote this row (or the empty row) directly
+  const int tid = threadIdx.x;
+  const int c = tid % D4;
+  const int slot = tid / D4;
+  QT *dst = reinterpret_cast<QT *>(p.out) + (int64_t)row * p.o_srow + (int64_t)h * p.o_shead;
+  const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
+  const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
+  float mx = -INFINITY;
+  for (int s = tid; s < n; s += 256) mx = fmaxf(mx, pm[(int64_t)s * p.pm_ssplit]);
+  red[tid] = mx;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  const float M = red[0];
+  const float msafe = (M == -INFINITY) ? 0.0f : M;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.0f;
+  const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 4 * c;
+  for (int s = slot; s < n; s += SLOTS) {
+    const float w = __builtin_amdgcn_exp2f(pm[(int64_t)s * p.pm_ssplit] - msafe) * pl[(int64_t)s * p.pl_ssplit];
+    f32x4 o;
+    if (p.po_f32) {
+      o = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p.po) + base + (int64_t)s * p.po_ssplit);
+    } else {
+      const _Float16 *src = reinterpret_cast<const _Float16 *>(p.po) + base + (int64_t)s * p.po_ssplit;
+      o = f32x4{(float)src[0], (float)src[1], (float)src[2], (float)src[3]};
+    }
+    acc += w * o;
+    wsum += w;
+  }
+  part[slot][c] = acc;
+  if (c == 0) wpart[slot] = wsum;
+  __syncthreads();
+  if (slot == 0) {
+    f32x4 o = part[0][c];
+    float W = wpart[0];
+    for (int s = 1; s < SLOTS; ++s) {
+      o += part[s][c];
+      W += wpart[s];
+    }
+    const float inv = (W > 0.0f) ? 1.0f / W : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[4 * c + e] = from_f32<QT>(o[e] * inv);
+    if (c == 0 && p.lse) {
+      p.lse[(int64_t)row * p.lse_srow + (int64_t)h * p.lse_shead] =
+          (W > 0.0f) ? kLn2 * (msafe + __builtin_amdgcn_logf(W)) : -INFINITY;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Bulk dequantisers (same conversions as the attention kernel)
+// ---------------------------------------------------------------------------
+__global__ void dequant_f32_kernel(const uint8_t *src, float *dst, int64_t n, float scale) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  int w = 0;
+  const int cnt = (n - i) < 4 ? (int)(n - i) : 4;
+  for (int e = 0; e < cnt; ++e) w |= (int)src[i + e] << (8 * e);
+  const f32x2 lo = fp8x2_f32(w, false);
+  const f32x2 hi = fp8x2_f32(w, true);
+  const float v[4] = {lo[0], lo[1], hi[0], hi[1]};
+  for (int e = 0; e < cnt; ++e) dst[i + e] = v[e] * scale;
+}
+
+__global__ void dequant_bf16_kernel(const uint8_t *src, uint16_t *dst, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  int w = 0;
+  const int cnt = (n - i) < 4 ? (int)(n - i) : 4;
+  for (int e = 0; e < cnt; ++e) w |= (int)src[i + e] << (8 * e);
+  bf16x8 v;
+  fp8x4_to(v, 0, w);
+  for (int e = 0; e < cnt; ++e) dst[i + e] = __builtin_bit_cast(uint16_t, v[e]);
+}
+
+}  // namespace l20pd
+
+// ===========================================================================
+// Host side: validation, launch, C ABI
+// ===========================================================================
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int32_t fail(int32_t code, const char *msg) {
+  snprintf(g_last_error, sizeof(g_last_error), "%s", msg);
+  return code;
+}
+
+int32_t check_args(const l20_pd_fp8_args *a) {
+  if (!a) return fail(L20_PD_EINVAL, "null argument block");
+  if (a->query_dtype != L20_PD_BF16 && a->query_dtype != L20_PD_FP16)
+    return fail(L20_PD_EINVAL, "query must be bf16 or fp16");
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(L20_PD_EINVAL, "NHD cache only: head_dim must be 64 or 128");
+  if (a->page_size != 16) return fail(L20_PD_EINVAL, "NHD cache only: page_size must be 16");
+  if (a->num_kv_heads <= 0 || a->num_q_heads <= 0)
+    return fail(L20_PD_EINVAL, "head counts must be positive");
+  if (a->num_q_heads % a->num_kv_heads != 0)
+    return fail(L20_PD_EINVAL, "Q heads must be divisible by KV heads");
+  if (a->q_len < 1) return fail(L20_PD_EINVAL, "q_len must be >= 1");
+  if ((a->num_q_heads / a->num_kv_heads) * a->q_len > 32)
+    return fail(L20_PD_EINVAL, "GQA group x q_len must be at most 32");
+  if (a->split_size < 64 || a->split_size > 1024 || a->split_size % 16 != 0)
+    return fail(L20_PD_EINVAL, "split_size must be a multiple of 16 from 64 through 1024");
+  if (a->batch < 0 || a->max_seq_len < 0) return fail(L20_PD_EINVAL, "batch and max_seq_len must be >= 0");
+  if (a->batch == 0) return L20_PD_OK;
+  if (!a->query || !a->key_cache || !a->value_cache || !a->block_table || !a->seq_lens || !a->output)
+    return fail(L20_PD_EINVAL, "null tensor pointer");
+  if (a->num_pages <= 0) return fail(L20_PD_EINVAL, "K/V cache has no pages");
+  const int32_t n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
+  if (n_s > 1) {
+    if (!a->partial_output || !a->partial_max || !a->partial_sum)
+      return fail(L20_PD_EINVAL, "partial output workspace has wrong shape");
+    if (a->partial_splits < n_s) return fail(L20_PD_EINVAL, "partial output workspace has wrong shape");
+    if (a->partial_dtype != L20_PD_FP32 && a->partial_dtype != L20_PD_FP16)
+      return fail(L20_PD_EINVAL, "partial output must be fp32 or fp16");
+  }
+  if (a->bt_max_pages * (int64_t)16 < a->max_seq_len)
+    return fail(L20_PD_EINVAL, "block table has fewer pages than max_seq_len needs");
+  // Vector-load alignment: 16 B K chunks, 8/4 B V chunks, 16 B query chunks.
+  const uint64_t kbits = (uint64_t)(uintptr_t)a->key_cache | (uint64_t)a->k_stride_page |
+                         (uint64_t)a->k_stride_token | (uint64_t)a->k_stride_head;
+  if (kbits % 16 != 0) return fail(L20_PD_EINVAL, "K cache pointer and strides must be 16-byte aligned");
+  const uint64_t vbits = (uint64_t)(uintptr_t)a->value_cache | (uint64_t)a->v_stride_page |
+                         (uint64_t)a->v_stride_token | (uint64_t)a->v_stride_head;
+  if (vbits % (a->head_dim == 128 ? 8u : 4u) != 0)
+    return fail(L20_PD_EINVAL, "V cache pointer and strides must be aligned to head_dim/16 bytes");
+  if (((uintptr_t)a->query % 16) != 0 || (a->q_stride_row % 8) != 0 || (a->q_stride_head % 8) != 0)
+    return fail(L20_PD_EINVAL, "query pointer and strides must be 16-byte aligned");
+  if (n_s > 1 && a->partial_dtype == L20_PD_FP32 &&
+      (((uintptr_t)a->partial_output % 16) != 0 || a->po_stride_row % 4 || a->po_stride_head % 4 ||
+       a->po_stride_split % 4))
+    return fail(L20_PD_EINVAL, "fp32 partial output must be 16-byte aligned");
+  return L20_PD_OK;
+}
+
+template <typename QT, int D, int NQT>
+hipError_t launch_partial(const l20pd::PartialParams &pp, int batch, int num_kv_heads, int nwaves,
+                          hipStream_t stream) {
+  dim3 grid(pp.num_splits, num_kv_heads, batch);
+  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), grid, dim3(64 * nwaves), 0, stream, pp);
+  return hipGetLastError();
+}
+
+template <typename QT, int D>
+hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipStream_t stream) {
+  hipLaunchKernelGGL((l20pd::pd_merge<QT, D>), dim3(heads, rows), dim3(256), 0, stream, mp);
+  return hipGetLastError();
+}
+
+l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
+  l20pd::PartialParams pp;
+  memset(&pp, 0, sizeof(pp));
+  pp.q = a.query;
+  pp.q_srow = a.q_stride_row;
+  pp.q_shead = a.q_stride_head;
+  pp.k = a.key_cache;
+  pp.k_spage = a.k_stride_page;
+  pp.k_stok = a.k_stride_token;
+  pp.k_shead = a.k_stride_head;
+  pp.v = a.value_cache;
+  pp.v_spage = a.v_stride_page;
+  pp.v_stok = a.v_stride_token;
+  pp.v_shead = a.v_stride_head;
+  pp.bt = a.block_table;
+  pp.bt_srow = a.bt_stride_row;
+  pp.seq_lens = a.seq_lens;
+  pp.num_pages = a.num_pages;
+  pp.po = a.partial_output;
+  pp.po_srow = a.po_stride_row;
+  pp.po_shead = a.po_stride_head;
+  pp.po_ssplit = a.po_stride_split;
+  pp.pm = a.partial_max;
+  pp.pm_srow = a.pm_stride_row;
+  pp.pm_shead = a.pm_stride_head;
+  pp.pm_ssplit = a.pm_stride_split;
+  pp.pl = a.partial_sum;
+  pp.pl_srow = a.ps_stride_row;
+  pp.pl_shead = a.ps_stride_head;
+  pp.pl_ssplit = a.ps_stride_split;
+  pp.out = a.output;
+  pp.o_srow = a.o_stride_row;
+  pp.o_shead = a.o_stride_head;
+  pp.lse = a.lse;
+  pp.lse_srow = a.lse_stride_row;
+  pp.lse_shead = a.lse_stride_head;
+  pp.k_scale = a.k_scale;
+  pp.v_scale = a.v_scale;
+  pp.k_scale_ph = a.k_scale_per_head;
+  pp.v_scale_ph = a.v_scale_per_head;
+  const float sm = a.softmax_scale > 0.0f ? a.softmax_scale : 1.0f / sqrtf((float)a.head_dim);
+  pp.qk_scale_log2 = sm * l20pd::kLog2e;
+  pp.q_len = a.q_len;
+  pp.num_q_heads = a.num_q_heads;
+  pp.num_kv_heads = a.num_kv_heads;
+  pp.group = a.num_q_heads / a.num_kv_heads;
+  pp.split_size = a.split_size;
+  pp.num_splits = n_s > 0 ? n_s : 1;
+  pp.po_f32 = a.partial_dtype == L20_PD_FP32;
+  const int64_t cap = std::min<int64_t>((int64_t)pp.num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
+  pp.l_cap = (int)cap;
+  return pp;
+}
+
+l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
+  l20pd::MergeParams mp;
+  memset(&mp, 0, sizeof(mp));
+  mp.po = a.partial_output;
+  mp.po_srow = a.po_stride_row;
+  mp.po_shead = a.po_stride_head;
+  mp.po_ssplit = a.po_stride_split;
+  mp.pm = a.partial_max;
+  mp.pm_srow = a.pm_stride_row;
+  mp.pm_shead = a.pm_stride_head;
+  mp.pm_ssplit = a.pm_stride_split;
+  mp.pl = a.partial_sum;
+  mp.pl_srow = a.ps_stride_row;
+  mp.pl_shead = a.ps_stride_head;
+  mp.pl_ssplit = a.ps_stride_split;
+  mp.seq_lens = a.seq_lens;
+  mp.out = a.output;
+  mp.o_srow = a.o_stride_row;
+  mp.o_shead = a.o_stride_head;
+  mp.lse = a.lse;
+  mp.lse_srow = a.lse_stride_row;
+  mp.lse_shead = a.lse_stride_head;
+  mp.q_len = a.q_len;
+  mp.split_size = a.split_size;
+  mp.num_splits = num_splits;
+  mp.po_f32 = a.partial_dtype == L20_PD_FP32;
+  mp.l_cap = (int)std::min<int64_t>((int64_t)num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
+  return mp;
+}
+
+// Which kernels one call enqueues.
+enum Stage { kPartial = 1, kMerge = 2, kBoth = 3 };
+
+int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages) {
+  g_last_error[0] = '\0';
+  const int32_t rc = check_args(a);
+  if (rc != L20_PD_OK) return rc;
+  if (a->batch == 0) return L20_PD_OK;
+  const int n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  const int group = a->num_q_heads / a->num_kv_heads;
+  const int nqt = (group * a->q_len + 15) / 16;
+  const int blocks_per_split = (a->split_size + 31) / 32;
+  const int nwaves = blocks_per_split >= 4 ? 4 : blocks_per_split;
+  const l20pd::PartialParams pp = partial_params(*a, n_s);
+  const l20pd::MergeParams mp = merge_params(*a, pp.num_splits);
+  const bool bf16 = a->query_dtype == L20_PD_BF16;
+  const int rows = a->batch * a->q_len;
+  hipError_t e = hipSuccess;
+  if (stages & kPartial) {
+    if (a->head_dim == 128) {
+      if (nqt == 1)
+        e = bf16 ? launch_partial<__bf16, 128, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream)
+                 : launch_partial<_Float16, 128, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+      else
+        e = bf16 ? launch_partial<__bf16, 128, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream)
+                 : launch_partial<_Float16, 128, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+    } else {
+      if (nqt == 1)
+        e = bf16 ? launch_partial<__bf16, 64, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream)
+                 : launch_partial<_Float16, 64, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+      else
+        e = bf16 ? launch_partial<__bf16, 64, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream)
+                 : launch_partial<_Float16, 64, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+    }
+  }
+  // With a single split every row is finished by the partial kernel.
+  if (e == hipSuccess && (stages & kMerge) && n_s > 1) {
+    if (a->head_dim == 128)
+      e = bf16 ? launch_merge<__bf16, 128>(mp, rows, a->num_q_heads, stream)
+               : launch_merge<_Float16, 128>(mp, rows, a->num_q_heads, stream);
+    else
+      e = bf16 ? launch_merge<__bf16, 64>(mp, rows, a->num_q_heads, stream)
+               : launch_merge<_Float16, 64>(mp, rows, a->num_q_heads, stream);
+  }
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t l20_pd_abi_version(void) { return L20_PD_ABI_VERSION; }
+
+const char *l20_pd_last_error(void) { return g_last_error; }
+
+int32_t l20_pd_num_splits(int32_t max_seq_len, int32_t split_size) {
+  if (max_seq_len <= 0 || split_size <= 0) return 0;
+  return (max_seq_len + split_size - 1) / split_size;
+}
+
+int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args) {
+  g_last_error[0] = '\0';
+  return check_args(args);
+}
+
+int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len, int32_t cu_count) {
+  if (cu_count <= 0) cu_count = 256;
+  const int64_t units = (int64_t)(batch > 0 ? batch : 1) * (num_kv_heads > 0 ? num_kv_heads : 1);
+  // Aim for >= 2 work items per CU; larger splits amortise the partial
+  // round trip, so take the largest split that still reaches that count.
+  const int64_t target = 2 * (int64_t)cu_count;
+  int32_t best = 64;
+  for (int32_t s = 1024; s >= 64; s -= 64) {
+    const int64_t items = units * (int64_t)l20_pd_num_splits(max_seq_len > 0 ? max_seq_len : 1, s);
+    if (items >= target) {
+      best = s;
+      break;
+    }
+  }
+  return best;
+}
+
+int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth); }
+
+int32_t l20_pd_fp8_e4m3_partial(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kPartial); }
+
+int32_t l20_pd_fp8_e4m3_merge(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kMerge); }
+
+int32_t l20_pd_fp8_e4m3_dequant_f32(const uint8_t *src, float *dst, int64_t n, float scale, void *stream) {
+  g_last_error[0] = '\0';
+  if (n < 0 || (n > 0 && (!src || !dst))) return fail(L20_PD_EINVAL, "invalid dequant arguments");
+  if (n == 0) return L20_PD_OK;
+  const int64_t threads = (n + 3) / 4;
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(L20_PD_EINVAL, "dequant size too large");
+  hipLaunchKernelGGL(l20pd::dequant_f32_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), src, dst, n, scale);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
+int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst, int64_t n, void *stream) {
+  g_last_error[0] = '\0';
+  if (n < 0 || (n > 0 && (!src || !dst))) return fail(L20_PD_EINVAL, "invalid dequant arguments");
+  if (n == 0) return L20_PD_OK;
+  const int64_t threads = (n + 3) / 4;
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(L20_PD_EINVAL, "dequant size too large");
+  hipLaunchKernelGGL(l20pd::dequant_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), src, dst, n);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
+}  // extern "C"

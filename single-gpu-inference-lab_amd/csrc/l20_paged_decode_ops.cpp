@@ -1,0 +1,198 @@
+// TORCH_LIBRARY(l20_stack) binding of the MI355X paged FP8 decode op.
+//
+// Keeps the reference's schema for paged_decode_fp8_e4m3_split_out verbatim
+// (integrations/vllm/cuda/l20_paged_decode.cpp:128-135, relative to the
+// reference repo root) and appends defaulted arguments, so every 13-argument
+// legacy call still binds:
+//   float? softmax_scale=None        (reference hard-codes 1/sqrt(128))
+//   Tensor? k_scale_per_head=None    (fp32 [Hkv]; overrides k_scale)
+//   Tensor? v_scale_per_head=None    (fp32 [Hkv]; overrides v_scale)
+//   int q_len=1                      (query rows [B*q_len, Hq, D], causal)
+//   Tensor(e!)? lse=None             (fp32 [B*q_len, Hq], natural log)
+// The implementation validates with the reference's TORCH_CHECK messages
+// (l20_paged_decode.cu:665-688) and calls the C ABI in
+// libl20_paged_decode_hip.so on the current HIP stream.  Nothing is
+// allocated: the caller owns the workspace, as in the reference.
+
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <c10/core/DeviceGuard.h>
+#include <torch/library.h>
+
+#include <optional>
+
+#include "l20_paged_decode.h"
+
+namespace {
+
+int32_t dtype_code(const at::Tensor &t) {
+  switch (t.scalar_type()) {
+    case at::kBFloat16:
+      return L20_PD_BF16;
+    case at::kHalf:
+      return L20_PD_FP16;
+    case at::kFloat:
+      return L20_PD_FP32;
+    default:
+      return -1;
+  }
+}
+
+void check_same_device(const at::Tensor &t, const at::Tensor &query, const char *what) {
+  TORCH_CHECK(t.device() == query.device(), what, " must be on the query's device");
+}
+
+at::Tensor paged_decode_fp8_e4m3_split_out(
+    const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache,
+    const at::Tensor &block_table, const at::Tensor &seq_lens, const at::Tensor &partial_output,
+    const at::Tensor &partial_max, const at::Tensor &partial_sum, const at::Tensor &output, double k_scale,
+    double v_scale, int64_t max_seq_len, int64_t split_size, std::optional<double> softmax_scale,
+    const std::optional<at::Tensor> &k_scale_per_head, const std::optional<at::Tensor> &v_scale_per_head,
+    int64_t q_len, const std::optional<at::Tensor> &lse) {
+  TORCH_CHECK(query.is_cuda(), "query must be CUDA");
+  TORCH_CHECK(query.scalar_type() == at::kBFloat16 || query.scalar_type() == at::kHalf,
+              "query must be bf16 or fp16");
+  TORCH_CHECK(key_cache.scalar_type() == at::kFloat8_e4m3fn && value_cache.scalar_type() == at::kFloat8_e4m3fn,
+              "K/V cache must be torch.float8_e4m3fn");
+  TORCH_CHECK(query.dim() == 3, "invalid query");
+  TORCH_CHECK(key_cache.dim() == 4 && key_cache.size(3) == query.size(2), "NHD cache only");
+  TORCH_CHECK(key_cache.sizes() == value_cache.sizes(), "K/V cache mismatch");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt, "int32 block table");
+  TORCH_CHECK(seq_lens.scalar_type() == at::kInt, "int32 sequence lengths");
+  TORCH_CHECK(q_len >= 1, "q_len must be >= 1");
+  TORCH_CHECK(query.size(1) % key_cache.size(2) == 0, "Q heads must be divisible by KV heads");
+  TORCH_CHECK(query.size(0) % q_len == 0, "query rows must be batch * q_len");
+  const int64_t rows = query.size(0);
+  const int64_t batch = rows / q_len;
+  const int64_t heads = query.size(1);
+  const int64_t head_dim = query.size(2);
+  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == batch, "block table must be [batch, max_pages]");
+  TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.size(0) == batch, "seq_lens must be [batch]");
+  TORCH_CHECK(block_table.stride(1) == 1 && seq_lens.is_contiguous(), "block table rows and seq_lens must be contiguous");
+  TORCH_CHECK(output.sizes() == query.sizes() && output.scalar_type() == query.scalar_type(),
+              "output must match the query's shape and dtype");
+  for (const at::Tensor *t : {&key_cache, &value_cache, &block_table, &seq_lens, &output})
+    check_same_device(*t, query, "every tensor");
+  TORCH_CHECK(query.stride(2) == 1 && key_cache.stride(3) == 1 && value_cache.stride(3) == 1 &&
+                  output.stride(2) == 1,
+              "head_dim must be the contiguous dimension");
+  const int64_t n_s = l20_pd_num_splits((int32_t)max_seq_len, (int32_t)split_size);
+  const bool need_ws = n_s > 1;
+  if (need_ws) {
+    TORCH_CHECK(partial_output.dim() == 4 && partial_output.size(0) == rows && partial_output.size(1) == heads &&
+                    partial_output.size(2) >= n_s && partial_output.size(3) == head_dim &&
+                    partial_output.stride(3) == 1,
+                "partial output workspace has wrong shape");
+    TORCH_CHECK(partial_output.scalar_type() == at::kFloat || partial_output.scalar_type() == at::kHalf,
+                "partial output workspace must be fp32 or fp16");
+    for (const at::Tensor *t : {&partial_max, &partial_sum}) {
+      TORCH_CHECK(t->dim() == 3 && t->size(0) == rows && t->size(1) == heads && t->size(2) >= n_s &&
+                      t->scalar_type() == at::kFloat,
+                  "partial max/sum workspace has wrong shape");
+      check_same_device(*t, query, "partial max/sum workspace");
+    }
+    check_same_device(partial_output, query, "partial output workspace");
+  }
+  const float *ksph = nullptr, *vsph = nullptr;
+  for (int which = 0; which < 2; ++which) {
+    const auto &opt = which == 0 ? k_scale_per_head : v_scale_per_head;
+    if (opt.has_value() && opt->defined()) {
+      const at::Tensor &t = *opt;
+      TORCH_CHECK(t.scalar_type() == at::kFloat && t.is_contiguous() && t.numel() == key_cache.size(2),
+                  "per-head scales must be contiguous fp32 [num_kv_heads]");
+      check_same_device(t, query, "per-head scales");
+      (which == 0 ? ksph : vsph) = t.data_ptr<float>();
+    }
+  }
+  float *lse_ptr = nullptr;
+  int64_t lse_srow = 0, lse_shead = 0;
+  if (lse.has_value() && lse->defined()) {
+    const at::Tensor &t = *lse;
+    TORCH_CHECK(t.scalar_type() == at::kFloat && t.dim() == 2 && t.size(0) == rows && t.size(1) == heads,
+                "lse must be fp32 [batch*q_len, num_q_heads]");
+    check_same_device(t, query, "lse");
+    lse_ptr = t.data_ptr<float>();
+    lse_srow = t.stride(0);
+    lse_shead = t.stride(1);
+  }
+
+  l20_pd_fp8_args a{};
+  a.query = query.data_ptr();
+  a.query_dtype = dtype_code(query);
+  a.q_stride_row = query.stride(0);
+  a.q_stride_head = query.stride(1);
+  a.key_cache = reinterpret_cast<const uint8_t *>(key_cache.data_ptr());
+  a.k_stride_page = key_cache.stride(0);
+  a.k_stride_token = key_cache.stride(1);
+  a.k_stride_head = key_cache.stride(2);
+  a.value_cache = reinterpret_cast<const uint8_t *>(value_cache.data_ptr());
+  a.v_stride_page = value_cache.stride(0);
+  a.v_stride_token = value_cache.stride(1);
+  a.v_stride_head = value_cache.stride(2);
+  a.num_pages = key_cache.size(0);
+  a.page_size = (int32_t)key_cache.size(1);
+  a.block_table = block_table.data_ptr<int32_t>();
+  a.bt_stride_row = block_table.stride(0);
+  a.bt_max_pages = (int32_t)block_table.size(1);
+  a.seq_lens = seq_lens.data_ptr<int32_t>();
+  if (need_ws) {
+    a.partial_output = partial_output.data_ptr();
+    a.partial_dtype = dtype_code(partial_output);
+    a.po_stride_row = partial_output.stride(0);
+    a.po_stride_head = partial_output.stride(1);
+    a.po_stride_split = partial_output.stride(2);
+    a.partial_splits = (int32_t)partial_output.size(2);
+    a.partial_max = partial_max.data_ptr<float>();
+    a.pm_stride_row = partial_max.stride(0);
+    a.pm_stride_head = partial_max.stride(1);
+    a.pm_stride_split = partial_max.stride(2);
+    a.partial_sum = partial_sum.data_ptr<float>();
+    a.ps_stride_row = partial_sum.stride(0);
+    a.ps_stride_head = partial_sum.stride(1);
+    a.ps_stride_split = partial_sum.stride(2);
+  }
+  a.output = output.data_ptr();
+  a.o_stride_row = output.stride(0);
+  a.o_stride_head = output.stride(1);
+  a.lse = lse_ptr;
+  a.lse_stride_row = lse_srow;
+  a.lse_stride_head = lse_shead;
+  a.k_scale = (float)k_scale;
+  a.v_scale = (float)v_scale;
+  a.k_scale_per_head = ksph;
+  a.v_scale_per_head = vsph;
+  a.softmax_scale = softmax_scale.has_value() ? (float)*softmax_scale : 0.0f;
+  a.batch = (int32_t)batch;
+  a.q_len = (int32_t)q_len;
+  a.num_q_heads = (int32_t)heads;
+  a.num_kv_heads = (int32_t)key_cache.size(2);
+  a.head_dim = (int32_t)head_dim;
+  a.max_seq_len = (int32_t)max_seq_len;
+  a.split_size = (int32_t)split_size;
+
+  const c10::DeviceGuard guard(query.device());
+  void *stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.get_device()).stream();
+  const int32_t rc = l20_pd_fp8_e4m3_split_out(&a, stream);
+  TORCH_CHECK(rc == L20_PD_OK, l20_pd_last_error());
+  return output;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(l20_stack, m) {
+  m.def(
+      "paged_decode_fp8_e4m3_split_out("
+      "Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, Tensor seq_lens, "
+      "Tensor(a!) partial_output, Tensor(b!) partial_max, "
+      "Tensor(c!) partial_sum, Tensor(d!) output, "
+      "float k_scale, float v_scale, "
+      "int max_seq_len, int split_size, "
+      "float? softmax_scale=None, Tensor? k_scale_per_head=None, "
+      "Tensor? v_scale_per_head=None, int q_len=1, "
+      "Tensor(e!)? lse=None) -> Tensor(d!)");
+}
+
+TORCH_LIBRARY_IMPL(l20_stack, CUDA, m) {
+  m.impl("paged_decode_fp8_e4m3_split_out", &paged_decode_fp8_e4m3_split_out);
+}

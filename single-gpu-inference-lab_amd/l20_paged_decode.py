@@ -1,0 +1,116 @@
+"""Dispatcher-backed entry point for the MI355X paged FP8 decode operator.
+
+Mirrors ``integrations/vllm/l20_paged_decode.py:1-117`` of the reference
+(paths relative to its repo root): ``load_library()`` loads
+``l20_paged_decode_ops.so`` from beside this file, ``paged_decode_fp8_e4m3_split_out``
+calls ``torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out`` and a
+``register_fake`` meta implementation returns ``output`` so the op traces
+under FakeTensor / torch.compile.  Both run at import.
+
+The native library is required: importing this module raises if the built
+``.so`` is missing, and the op has no CPU implementation to fall back on.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+from typing import Optional, Union
+
+import torch
+
+_LIB_NAME = "l20_paged_decode_ops.so"
+_loaded = False
+
+
+def library_path() -> Path:
+    return Path(__file__).with_name(_LIB_NAME)
+
+
+def load_library(path: Optional[Union[str, Path]] = None) -> None:
+    """Load the TORCH_LIBRARY(l20_stack) extension (idempotent)."""
+    global _loaded
+    library = Path(path) if path is not None else library_path()
+    if not library.exists():
+        raise ImportError(
+            f"{library} is missing: build it with `python {Path(__file__).with_name('l20_pd_build.py')}`"
+        )
+    if _loaded and path is None:
+        return
+    torch.ops.load_library(str(library))
+    _loaded = True
+
+
+def paged_decode_fp8_e4m3_split_out(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    partial_output: torch.Tensor,
+    partial_max: torch.Tensor,
+    partial_sum: torch.Tensor,
+    output: torch.Tensor,
+    k_scale: float,
+    v_scale: float,
+    max_seq_len: int,
+    split_size: int,
+    softmax_scale: Optional[float] = None,
+    k_scale_per_head: Optional[torch.Tensor] = None,
+    v_scale_per_head: Optional[torch.Tensor] = None,
+    q_len: int = 1,
+    lse: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Paged FP8 e4m3fn split-KV decode attention; writes and returns ``output``.
+
+    The first 13 arguments are the reference's (``l20_paged_decode.py:48-77``);
+    the rest extend it (see the op schema).
+    """
+    return torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
+        query,
+        key_cache,
+        value_cache,
+        block_table,
+        seq_lens,
+        partial_output,
+        partial_max,
+        partial_sum,
+        output,
+        float(k_scale),
+        float(v_scale),
+        int(max_seq_len),
+        int(split_size),
+        None if softmax_scale is None else float(softmax_scale),
+        k_scale_per_head,
+        v_scale_per_head,
+        int(q_len),
+        lse,
+    )
+
+
+def _register_fake() -> None:
+    @torch.library.register_fake("l20_stack::paged_decode_fp8_e4m3_split_out")
+    def _paged_decode_fp8_e4m3_split_out_fake(
+        query,
+        key_cache,
+        value_cache,
+        block_table,
+        seq_lens,
+        partial_output,
+        partial_max,
+        partial_sum,
+        output,
+        k_scale,
+        v_scale,
+        max_seq_len,
+        split_size,
+        softmax_scale=None,
+        k_scale_per_head=None,
+        v_scale_per_head=None,
+        q_len=1,
+        lse=None,
+    ):
+        return output
+
+
+load_library()
+_register_fake()

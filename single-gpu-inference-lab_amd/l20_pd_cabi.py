@@ -1,0 +1,172 @@
+"""ctypes binding of the C ABI in ``include/l20_paged_decode.h``.
+
+Loads ``libl20_paged_decode_hip.so`` from beside this file and mirrors the
+``l20_pd_fp8_args`` struct field by field.  ``args_from_tensors`` fills the
+struct from torch tensors (device pointers, sizes, strides) so that tests and
+benchmarks can call the library without the torch dispatcher in between.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+LIB_PATH = Path(__file__).with_name("libl20_paged_decode_hip.so")
+
+L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
+L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
+
+# Every extern "C" symbol declared in include/l20_paged_decode.h.
+EXPORTED = (
+    "l20_pd_abi_version",
+    "l20_pd_last_error",
+    "l20_pd_num_splits",
+    "l20_pd_fp8_e4m3_check",
+    "l20_pd_fp8_e4m3_split_out",
+    "l20_pd_fp8_e4m3_partial",
+    "l20_pd_fp8_e4m3_merge",
+    "l20_pd_default_split_size",
+    "l20_pd_fp8_e4m3_dequant_f32",
+    "l20_pd_fp8_e4m3_dequant_bf16",
+)
+
+_i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+
+class L20PdFp8Args(ctypes.Structure):
+    _fields_ = [
+        ("query", _vp), ("query_dtype", _i32), ("q_stride_row", _i64), ("q_stride_head", _i64),
+        ("key_cache", _vp), ("k_stride_page", _i64), ("k_stride_token", _i64), ("k_stride_head", _i64),
+        ("value_cache", _vp), ("v_stride_page", _i64), ("v_stride_token", _i64), ("v_stride_head", _i64),
+        ("num_pages", _i64), ("page_size", _i32),
+        ("block_table", _vp), ("bt_stride_row", _i64), ("bt_max_pages", _i32),
+        ("seq_lens", _vp),
+        ("partial_output", _vp), ("partial_dtype", _i32),
+        ("po_stride_row", _i64), ("po_stride_head", _i64), ("po_stride_split", _i64),
+        ("partial_splits", _i32),
+        ("partial_max", _vp), ("pm_stride_row", _i64), ("pm_stride_head", _i64), ("pm_stride_split", _i64),
+        ("partial_sum", _vp), ("ps_stride_row", _i64), ("ps_stride_head", _i64), ("ps_stride_split", _i64),
+        ("output", _vp), ("o_stride_row", _i64), ("o_stride_head", _i64),
+        ("lse", _vp), ("lse_stride_row", _i64), ("lse_stride_head", _i64),
+        ("k_scale", _f32), ("v_scale", _f32),
+        ("k_scale_per_head", _vp), ("v_scale_per_head", _vp),
+        ("softmax_scale", _f32),
+        ("batch", _i32), ("q_len", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
+        ("max_seq_len", _i32), ("split_size", _i32),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load the C ABI library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    lib_path = Path(path) if path else LIB_PATH
+    if not lib_path.exists():
+        raise OSError(f"{lib_path} is missing: build it with l20_pd_build.py")
+    lib = ctypes.CDLL(str(lib_path))
+    lib.l20_pd_abi_version.restype = _i32
+    lib.l20_pd_last_error.restype = ctypes.c_char_p
+    lib.l20_pd_num_splits.argtypes = [_i32, _i32]
+    lib.l20_pd_num_splits.restype = _i32
+    args_p = ctypes.POINTER(L20PdFp8Args)
+    lib.l20_pd_fp8_e4m3_check.argtypes = [args_p]
+    lib.l20_pd_fp8_e4m3_check.restype = _i32
+    for name in ("l20_pd_fp8_e4m3_split_out", "l20_pd_fp8_e4m3_partial", "l20_pd_fp8_e4m3_merge"):
+        getattr(lib, name).argtypes = [args_p, _vp]
+        getattr(lib, name).restype = _i32
+    lib.l20_pd_default_split_size.argtypes = [_i32, _i32, _i32, _i32]
+    lib.l20_pd_default_split_size.restype = _i32
+    lib.l20_pd_fp8_e4m3_dequant_f32.argtypes = [_vp, _vp, _i64, _f32, _vp]
+    lib.l20_pd_fp8_e4m3_dequant_f32.restype = _i32
+    lib.l20_pd_fp8_e4m3_dequant_bf16.argtypes = [_vp, _vp, _i64, _vp]
+    lib.l20_pd_fp8_e4m3_dequant_bf16.restype = _i32
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error(lib: Optional[ctypes.CDLL] = None) -> str:
+    return (lib or load()).l20_pd_last_error().decode()
+
+
+def _dtype_code(t) -> int:
+    import torch
+
+    return {torch.bfloat16: L20_PD_BF16, torch.float16: L20_PD_FP16, torch.float32: L20_PD_FP32}[t.dtype]
+
+
+def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, partial_output, partial_max,
+                      partial_sum, output, k_scale, v_scale, max_seq_len, split_size, *, softmax_scale=None,
+                      k_scale_per_head=None, v_scale_per_head=None, q_len=1, lse=None) -> L20PdFp8Args:
+    """Fill ``l20_pd_fp8_args`` from tensors (same argument order as the op)."""
+    a = L20PdFp8Args()
+    a.query = query.data_ptr()
+    a.query_dtype = _dtype_code(query)
+    a.q_stride_row, a.q_stride_head = query.stride(0), query.stride(1)
+    a.key_cache = key_cache.data_ptr()
+    a.k_stride_page, a.k_stride_token, a.k_stride_head = key_cache.stride()[:3]
+    a.value_cache = value_cache.data_ptr()
+    a.v_stride_page, a.v_stride_token, a.v_stride_head = value_cache.stride()[:3]
+    a.num_pages, a.page_size = key_cache.shape[0], key_cache.shape[1]
+    a.block_table = block_table.data_ptr()
+    a.bt_stride_row, a.bt_max_pages = block_table.stride(0), block_table.shape[1]
+    a.seq_lens = seq_lens.data_ptr()
+    if partial_output is not None:
+        a.partial_output = partial_output.data_ptr()
+        a.partial_dtype = _dtype_code(partial_output)
+        a.po_stride_row, a.po_stride_head, a.po_stride_split = partial_output.stride()[:3]
+        a.partial_splits = partial_output.shape[2]
+        a.partial_max = partial_max.data_ptr()
+        a.pm_stride_row, a.pm_stride_head, a.pm_stride_split = partial_max.stride()
+        a.partial_sum = partial_sum.data_ptr()
+        a.ps_stride_row, a.ps_stride_head, a.ps_stride_split = partial_sum.stride()
+    a.output = output.data_ptr()
+    a.o_stride_row, a.o_stride_head = output.stride(0), output.stride(1)
+    if lse is not None:
+        a.lse = lse.data_ptr()
+        a.lse_stride_row, a.lse_stride_head = lse.stride()
+    a.k_scale, a.v_scale = float(k_scale), float(v_scale)
+    if k_scale_per_head is not None:
+        a.k_scale_per_head = k_scale_per_head.data_ptr()
+    if v_scale_per_head is not None:
+        a.v_scale_per_head = v_scale_per_head.data_ptr()
+    a.softmax_scale = 0.0 if softmax_scale is None else float(softmax_scale)
+    a.batch = query.shape[0] // q_len
+    a.q_len = q_len
+    a.num_q_heads, a.head_dim = query.shape[1], query.shape[2]
+    a.num_kv_heads = key_cache.shape[2]
+    a.max_seq_len, a.split_size = int(max_seq_len), int(split_size)
+    return a
+
+
+def _call(name: str, args: L20PdFp8Args, stream: int, lib: Optional[ctypes.CDLL]) -> None:
+    lib = lib or load()
+    rc = getattr(lib, name)(ctypes.byref(args), ctypes.c_void_p(stream))
+    if rc != L20_PD_OK:
+        raise RuntimeError(last_error(lib))
+
+
+def split_out(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
+    """Call ``l20_pd_fp8_e4m3_split_out``; raise RuntimeError with the library's message on failure."""
+    _call("l20_pd_fp8_e4m3_split_out", args, stream, lib)
+
+
+def partial(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
+    """Enqueue only the split-KV partial kernel."""
+    _call("l20_pd_fp8_e4m3_partial", args, stream, lib)
+
+
+def merge(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
+    """Enqueue only the LSE merge kernel."""
+    _call("l20_pd_fp8_e4m3_merge", args, stream, lib)
+
+
+def check(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> None:
+    lib = lib or load()
+    if lib.l20_pd_fp8_e4m3_check(ctypes.byref(args)) != L20_PD_OK:
+        raise RuntimeError(last_error(lib))

@@ -1,0 +1,159 @@
+"""Helpers shared by the GPU parity tests, smoke() and bench.py's checks:
+build seeded inputs, run the HIP op (torch dispatcher or C ABI), run the CPU
+oracle on the same bytes, and compare to the stated tolerances.
+
+Tolerances (bf16/fp16 output vs the fp32 dequantise-then-attend oracle):
+max |diff| <= 1e-2 and per-(row, head) cosine >= 0.9999; natural-log LSE
+|diff| <= 1e-4 * max(1, |lse|).  FP8 -> fp32 dequantisation is exact, so only
+accumulation order (and the f16 rounding of softmax probabilities on the MFMA
+path) separates the two.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (str(ROOT / "single-gpu-inference-lab_amd"), str(ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+OUT_ATOL = 1e-2
+COS_MIN = 0.9999
+LSE_RTOL = 1e-4
+
+
+def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, device="cuda",
+                   dtype=torch.bfloat16, pool_extra=7, max_pages=None, garbage_tail=False):
+    """Seeded paged inputs of an arbitrary shape (generated on CPU, copied to ``device``)."""
+    import l20_pd_workloads as wl
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.as_tensor(lens, dtype=torch.int32)
+    pages_per = (lens.to(torch.int64) + 15) // 16
+    pool = int(pages_per.sum()) + pool_extra
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    mp = max(1, int(pages_per.max())) if max_pages is None else max_pages
+    table = torch.full((batch, mp), -7, dtype=torch.int32)  # unused entries are garbage
+    off = 0
+    for b in range(batch):
+        n = int(pages_per[b])
+        table[b, :n] = perm[off:off + n]
+        off += n
+    query = torch.randn(batch * q_len, hq, d, generator=g).to(dtype)
+    caches = []
+    for _ in range(2):
+        raw = torch.randn(pool, 16, hkv, d, generator=g).to(torch.bfloat16)
+        codes, scale = wl.quantize_fp8_e4m3(raw, per_head_axis=2 if per_head else None)
+        if garbage_tail:
+            # bytes beyond each sequence's end in its last page: NaN codes
+            u8 = codes.view(torch.uint8)
+            for b in range(batch):
+                L = int(lens[b])
+                if L % 16:
+                    u8[int(table[b, L // 16]), L % 16:] = 0x7F
+        caches.append((codes, scale))
+    (kc, ks), (vc, vs) = caches
+    return {
+        "query": query.to(device), "key_cache": kc.to(device), "value_cache": vc.to(device),
+        "block_table": table.to(device), "seq_lens": lens.to(device),
+        "k_scale": ks if isinstance(ks, float) else ks.to(device),
+        "v_scale": vs if isinstance(vs, float) else vs.to(device),
+        "softmax_scale": d ** -0.5, "q_len": q_len, "max_seq_len": int(lens.max()) if len(lens) else 0,
+    }
+
+
+def _scales(x):
+    return (x, None) if isinstance(x, float) else (1.0, x)
+
+
+def workspace(inp, split_size, partial_dtype=torch.float32, extra_splits=0):
+    import math
+
+    q = inp["query"]
+    n_s = max(1, math.ceil(inp["max_seq_len"] / split_size)) + extra_splits
+    rows, hq, d = q.shape
+    return (torch.empty(rows, hq, n_s, d, dtype=partial_dtype, device=q.device),
+            torch.empty(rows, hq, n_s, dtype=torch.float32, device=q.device),
+            torch.empty(rows, hq, n_s, dtype=torch.float32, device=q.device))
+
+
+def run_op(inp, split_size, *, via="torch", partial_dtype=torch.float32, with_lse=True, key_cache=None,
+           value_cache=None, output=None):
+    """Run the HIP op on ``inp``; returns ``(out, lse)`` (device tensors)."""
+    import l20_paged_decode  # noqa: F401
+    import l20_pd_cabi as cabi
+
+    q = inp["query"]
+    kc = inp["key_cache"] if key_cache is None else key_cache
+    vc = inp["value_cache"] if value_cache is None else value_cache
+    po, pm, ps = workspace(inp, split_size, partial_dtype)
+    out = torch.empty_like(q) if output is None else output
+    lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device) if with_lse else None
+    ks, ksph = _scales(inp["k_scale"])
+    vs, vsph = _scales(inp["v_scale"])
+    if via == "torch":
+        torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
+            q, kc, vc, inp["block_table"], inp["seq_lens"], po, pm, ps, out, ks, vs,
+            inp["max_seq_len"], split_size, inp["softmax_scale"], ksph, vsph, inp["q_len"], lse)
+    else:
+        args = cabi.args_from_tensors(
+            q, kc, vc, inp["block_table"], inp["seq_lens"], po, pm, ps, out, ks, vs, inp["max_seq_len"],
+            split_size, softmax_scale=inp["softmax_scale"], k_scale_per_head=ksph, v_scale_per_head=vsph,
+            q_len=inp["q_len"], lse=lse)
+        cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def run_oracle(inp, rows: Optional[Sequence[int]] = None):
+    """The CPU oracle on the same bytes; returns numpy ``(out, lse)``."""
+    from oracle import paged_fp8_decode_ref as ref
+
+    def host_scale(s):
+        return s if isinstance(s, float) else s.float().cpu().numpy()
+
+    return ref.reference(
+        inp["query"].float().cpu().numpy(),
+        inp["key_cache"].view(torch.uint8).cpu().numpy(),
+        inp["value_cache"].view(torch.uint8).cpu().numpy(),
+        inp["block_table"].cpu().numpy(),
+        inp["seq_lens"].cpu().numpy(),
+        host_scale(inp["k_scale"]), host_scale(inp["v_scale"]),
+        softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows)
+
+
+def compare(out, lse, exp_out, exp_lse, rows: Optional[np.ndarray] = None, check_lse=True):
+    """Assert the tolerances; returns a dict of the observed errors."""
+    got = out.float().cpu().numpy()
+    got_lse = lse.cpu().numpy() if lse is not None else None
+    if rows is not None:
+        got, exp_out = got[rows], exp_out[rows]
+        if got_lse is not None:
+            got_lse, exp_lse = got_lse[rows], exp_lse[rows]
+    assert np.all(np.isfinite(got)), "non-finite output"
+    diff = np.abs(got - exp_out)
+    max_abs = float(diff.max()) if diff.size else 0.0
+    num = (got * exp_out).sum(-1)
+    den = np.linalg.norm(got, axis=-1) * np.linalg.norm(exp_out, axis=-1)
+    nz = den > 0
+    cos = np.where(nz, num / np.where(nz, den, 1.0), 1.0)
+    # rows whose expected output is exactly zero must be zero too
+    assert np.all(np.abs(got[~nz]) <= OUT_ATOL)
+    min_cos = float(cos.min()) if cos.size else 1.0
+    res = {"max_abs": max_abs, "min_cos": min_cos}
+    assert max_abs <= OUT_ATOL, res
+    assert min_cos >= COS_MIN, res
+    if check_lse and got_lse is not None:
+        both_inf = np.isneginf(got_lse) & np.isneginf(exp_lse)
+        assert np.array_equal(np.isneginf(got_lse), np.isneginf(exp_lse)), "LSE -inf pattern differs"
+        fin = ~both_inf
+        err = np.abs(got_lse[fin] - exp_lse[fin]) / np.maximum(1.0, np.abs(exp_lse[fin]))
+        res["lse_rel"] = float(err.max()) if err.size else 0.0
+        assert res["lse_rel"] <= LSE_RTOL, res
+    return res

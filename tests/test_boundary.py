@@ -1,0 +1,218 @@
+"""The drop-in boundary on CPU: C ABI exports and validation, the torch op
+schema and fake implementation, and the hook-facing Python API's contract.
+No kernel is launched here.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import l20_pd_cabi as cabi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "l20_paged_decode.h"
+HIP_SRC = ROOT / "single-gpu-inference-lab_amd" / "csrc" / "l20_paged_decode_fp8.hip"
+OPS_SRC = ROOT / "single-gpu-inference-lab_amd" / "csrc" / "l20_paged_decode_ops.cpp"
+
+REFERENCE_SCHEMA_PREFIX = (
+    "l20_stack::paged_decode_fp8_e4m3_split_out(Tensor query, Tensor key_cache, Tensor value_cache, "
+    "Tensor block_table, Tensor seq_lens, Tensor(a!) partial_output, Tensor(b!) partial_max, "
+    "Tensor(c!) partial_sum, Tensor(d!) output, float k_scale, float v_scale, int max_seq_len, "
+    "int split_size"
+)
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(l20_pd_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = cabi.load()
+    declared = header_functions()
+    assert declared, "no declarations parsed from the header"
+    assert sorted(cabi.EXPORTED) == declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.l20_pd_abi_version() == 1
+
+
+def test_num_splits_and_default_split_size():
+    lib = cabi.load()
+    assert lib.l20_pd_num_splits(257, 128) == 3
+    assert lib.l20_pd_num_splits(256, 128) == 2
+    assert lib.l20_pd_num_splits(0, 128) == 0
+    for b, h, s in [(128, 4, 8192), (2, 8, 131072), (4, 2, 512), (1, 1, 16)]:
+        split = lib.l20_pd_default_split_size(b, h, s, 256)
+        assert 64 <= split <= 1024 and split % 16 == 0
+    # long single sequences get the largest split that still fills the chip
+    assert lib.l20_pd_default_split_size(2, 8, 131072, 256) == 1024
+
+
+def valid_args():
+    """A well-formed argument block with fake (never dereferenced) pointers."""
+    a = cabi.L20PdFp8Args()
+    fake = 0x10000
+    a.query, a.query_dtype, a.q_stride_row, a.q_stride_head = fake, cabi.L20_PD_BF16, 28 * 128, 128
+    a.key_cache, a.k_stride_page, a.k_stride_token, a.k_stride_head = fake, 16 * 4 * 128, 4 * 128, 128
+    a.value_cache, a.v_stride_page, a.v_stride_token, a.v_stride_head = fake, 16 * 4 * 128, 4 * 128, 128
+    a.num_pages, a.page_size = 1000, 16
+    a.block_table, a.bt_stride_row, a.bt_max_pages = fake, 64, 64
+    a.seq_lens = fake
+    a.partial_output, a.partial_dtype = fake, cabi.L20_PD_FP32
+    a.po_stride_row, a.po_stride_head, a.po_stride_split, a.partial_splits = 28 * 4 * 128, 4 * 128, 128, 4
+    a.partial_max, a.pm_stride_row, a.pm_stride_head, a.pm_stride_split = fake, 28 * 4, 4, 1
+    a.partial_sum, a.ps_stride_row, a.ps_stride_head, a.ps_stride_split = fake, 28 * 4, 4, 1
+    a.output, a.o_stride_row, a.o_stride_head = fake, 28 * 128, 128
+    a.k_scale = a.v_scale = 0.01
+    a.batch, a.q_len, a.num_q_heads, a.num_kv_heads, a.head_dim = 8, 1, 28, 4, 128
+    a.max_seq_len, a.split_size = 1024, 256
+    return a
+
+
+def test_check_accepts_valid_arguments():
+    cabi.check(valid_args())
+
+
+BAD = [
+    ("split_size", 48, "split_size must be a multiple of 16 from 64 through 1024"),
+    ("split_size", 1040, "split_size must be a multiple of 16 from 64 through 1024"),
+    ("split_size", 72, "split_size must be a multiple of 16 from 64 through 1024"),
+    ("num_q_heads", 30, "Q heads must be divisible by KV heads"),
+    ("partial_splits", 3, "partial output workspace has wrong shape"),
+    ("partial_output", 0, "partial output workspace has wrong shape"),
+    ("head_dim", 96, "NHD cache only"),
+    ("page_size", 32, "NHD cache only"),
+    ("query_dtype", cabi.L20_PD_FP32, "query must be bf16 or fp16"),
+    ("q_len", 0, "q_len must be >= 1"),
+    ("q_len", 5, "GQA group x q_len must be at most 32"),
+    ("k_stride_token", 4 * 128 + 8, "K cache pointer and strides must be 16-byte aligned"),
+    ("v_stride_head", 130, "V cache pointer and strides must be aligned"),
+    ("q_stride_head", 132, "query pointer and strides must be 16-byte aligned"),
+    ("bt_max_pages", 63, "block table has fewer pages than max_seq_len needs"),
+    ("query", 0, "null tensor pointer"),
+    ("num_pages", 0, "K/V cache has no pages"),
+]
+
+
+@pytest.mark.parametrize("field,value,message", BAD)
+def test_check_rejects_bad_arguments(field, value, message):
+    a = valid_args()
+    setattr(a, field, value)
+    with pytest.raises(RuntimeError, match=re.escape(message)):
+        cabi.check(a)
+    # the launching entry point validates identically and enqueues nothing
+    lib = cabi.load()
+    assert lib.l20_pd_fp8_e4m3_split_out(ctypes.byref(a), None) == cabi.L20_PD_EINVAL
+    assert message in cabi.last_error(lib)
+
+
+def test_single_split_needs_no_workspace():
+    a = valid_args()
+    a.max_seq_len, a.split_size = 200, 256
+    a.partial_output = a.partial_max = a.partial_sum = 0
+    cabi.check(a)
+
+
+def test_empty_batch_is_a_noop():
+    a = valid_args()
+    a.batch = 0
+    lib = cabi.load()
+    assert lib.l20_pd_fp8_e4m3_split_out(ctypes.byref(a), None) == cabi.L20_PD_OK
+
+
+# ------------------------------------------------------------------ torch op
+def test_torch_op_keeps_reference_schema_and_extends_it():
+    import l20_paged_decode  # noqa: F401
+
+    schema = str(torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out.default._schema)
+    assert schema.startswith(REFERENCE_SCHEMA_PREFIX)
+    for extra in ("float? softmax_scale=None", "Tensor? k_scale_per_head=None", "Tensor? v_scale_per_head=None",
+                  "int q_len=1", "Tensor(e!)? lse=None"):
+        assert extra in schema
+    assert schema.endswith("-> Tensor(d!)")
+
+
+def _meta_inputs(rows=4, hq=8, hkv=2, d=128, pages=32, splits=3):
+    m = dict(device="meta")
+    return (
+        torch.empty(rows, hq, d, dtype=torch.bfloat16, **m),
+        torch.empty(pages, 16, hkv, d, dtype=torch.float8_e4m3fn, **m),
+        torch.empty(pages, 16, hkv, d, dtype=torch.float8_e4m3fn, **m),
+        torch.empty(rows, 8, dtype=torch.int32, **m),
+        torch.empty(rows, dtype=torch.int32, **m),
+        torch.empty(rows, hq, splits, d, dtype=torch.float32, **m),
+        torch.empty(rows, hq, splits, dtype=torch.float32, **m),
+        torch.empty(rows, hq, splits, dtype=torch.float32, **m),
+        torch.empty(rows, hq, d, dtype=torch.bfloat16, **m),
+    )
+
+
+def test_fake_impl_returns_output_alias_on_meta_tensors():
+    import l20_paged_decode
+
+    args = _meta_inputs()
+    out = l20_paged_decode.paged_decode_fp8_e4m3_split_out(*args, 0.1, 0.1, 128, 64)
+    assert out.shape == args[-1].shape and out.dtype == torch.bfloat16 and out.device.type == "meta"
+    # legacy 13-positional-argument call through the dispatcher
+    out2 = torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(*args, 0.1, 0.1, 128, 64)
+    assert out2.shape == args[-1].shape
+
+
+def test_fake_impl_traces_under_fake_tensor_mode():
+    import l20_paged_decode
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode() as mode:
+        args = [mode.from_tensor(torch.empty(t.shape, dtype=t.dtype)) for t in _meta_inputs()]
+        out = l20_paged_decode.paged_decode_fp8_e4m3_split_out(*args, 0.1, 0.1, 128, 64, q_len=2)
+        assert out.shape == args[-1].shape
+
+
+def test_op_rejects_cpu_query_with_reference_message():
+    import l20_paged_decode  # noqa: F401
+
+    args = [torch.empty(t.shape, dtype=t.dtype) for t in _meta_inputs()]
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(*args, 0.1, 0.1, 128, 64)
+
+
+# ------------------------------------------------------------------ hook API
+def test_hook_api_requires_mi355x_and_fp8_cache():
+    import l20_paged_split_kv as sk
+
+    q = torch.empty(2, 8, 128, dtype=torch.bfloat16)
+    kv = torch.empty(4, 16, 2, 128, dtype=torch.float8_e4m3fn)
+    with pytest.raises(RuntimeError, match="requires an MI355X"):
+        sk.l20_paged_split_kv_attention_fp8(q, kv, kv, torch.zeros(2, 4, dtype=torch.int32),
+                                            torch.ones(2, dtype=torch.int32), k_scale=1.0, v_scale=1.0)
+    assert sk.should_use_l20_paged_fp8_split_kv(8, 4096) is False  # no GPU here
+
+
+def test_workspace_allocation_shapes():
+    import l20_paged_split_kv as sk
+
+    q = torch.empty(12, 28, 128, dtype=torch.bfloat16)
+    po, pm, ps, out = sk.allocate_l20_paged_split_kv_workspace(q, 1000, split_size=256)
+    assert po.shape == (12, 28, 4, 128) and po.dtype == torch.float32
+    assert pm.shape == ps.shape == (12, 28, 4)
+    assert out.shape == q.shape and out.dtype == q.dtype
+
+
+# ------------------------------------------------------------------ source contracts
+def test_kernel_source_contracts():
+    """The reference's source-string contract (tests/test_cuda_paged_decode_source.py:4-37),
+    restated for this build's kernel and binding names."""
+    src = HIP_SRC.read_text()
+    ops = OPS_SRC.read_text()
+    for name in ("pd_fp8_partial", "pd_merge", "split_size must be a multiple of 16 from 64 through 1024",
+                 "Q heads must be divisible by KV heads", "partial output workspace has wrong shape",
+                 "v_mfma", "__builtin_amdgcn_mfma_f32_16x16x32_bf16"):
+        assert name in src, name
+    for needle in ("TORCH_LIBRARY(l20_stack", "TORCH_LIBRARY_IMPL(l20_stack, CUDA", "query must be CUDA",
+                   "K/V cache must be torch.float8_e4m3fn", "int32 block table", "int32 sequence lengths"):
+        assert needle in ops, needle
+    assert "hipMalloc" not in src and "hipMemset" not in src  # the op allocates nothing

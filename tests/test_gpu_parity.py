@@ -1,0 +1,211 @@
+"""GPU parity: the HIP kernels against the CPU oracle on identical bytes.
+
+Every test calls the library either through the torch dispatcher
+(``torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out``) or straight through
+the C ABI (ctypes).  Tolerances are the ones in ``pd_helpers``.
+"""
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import pd_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X GPU")
+    import l20_paged_decode  # noqa: F401  (fails loudly if the extension is missing)
+
+
+# ------------------------------------------------------------ conversions
+def test_fp8_conversions_match_oracle_table_on_all_codes():
+    from oracle import paged_fp8_decode_ref as ref
+    import l20_pd_cabi as cabi
+
+    lib = cabi.load()
+    codes = torch.arange(256, dtype=torch.uint8).repeat(3).cuda()  # 768: exercises the 4-byte tail
+    codes = torch.cat([codes, codes[:3]])
+    f32 = torch.empty(codes.numel(), dtype=torch.float32, device="cuda")
+    bf = torch.empty(codes.numel(), dtype=torch.int16, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.l20_pd_fp8_e4m3_dequant_f32(codes.data_ptr(), f32.data_ptr(), codes.numel(), 1.0, s) == 0
+    assert lib.l20_pd_fp8_e4m3_dequant_bf16(codes.data_ptr(), bf.data_ptr(), codes.numel(), s) == 0
+    torch.cuda.synchronize()
+    table = ref.e4m3fn_decode_table()
+    want = table[codes.cpu().numpy()]
+    got = f32.cpu().numpy()
+    got_bf = bf.cpu().view(torch.bfloat16).float().numpy()
+    nan = np.isnan(want)
+    for g in (got, got_bf):
+        assert np.array_equal(np.isnan(g), nan)
+        assert np.array_equal(g[~nan], want[~nan])
+        assert np.array_equal(np.signbit(g[~nan]), np.signbit(want[~nan]))
+    # scaled dequantisation is code * scale in fp32
+    assert lib.l20_pd_fp8_e4m3_dequant_f32(codes.data_ptr(), f32.data_ptr(), codes.numel(), 0.37, s) == 0
+    torch.cuda.synchronize()
+    scaled = f32.cpu().numpy()
+    assert np.array_equal(scaled[~nan], (want[~nan] * np.float32(0.37)).astype(np.float32))
+
+
+# ------------------------------------------------------------ the five configurations
+CONFIG_SPLITS = {
+    "c1_qwen2.5_0.5b": [64, 512],
+    "c2_qwen2.5_coder_3b": [256, 1024],
+    "c3_qwen2.5_7b": [512, 1024],
+    "c4_llama3_8b_long": [1024],
+    "c5_llama3_70b_verify": [512],
+}
+ORACLE_ROWS = {"c5_llama3_70b_verify": [0, 17, 63]}
+
+
+@pytest.mark.parametrize("name", list(CONFIG_SPLITS))
+def test_config_parity(name):
+    import l20_pd_workloads as wl
+
+    cfg = wl.CONFIGS[name]
+    inp = wl.make_inputs(cfg, device="cuda")
+    inp["query"] = inp["query"].contiguous()
+    rows_b = ORACLE_ROWS.get(name)
+    exp_out, exp_lse = H.run_oracle(inp, rows=rows_b)
+    rows = None
+    if rows_b is not None:
+        rows = np.concatenate([np.arange(b * cfg.q_len, (b + 1) * cfg.q_len) for b in rows_b])
+    for split in CONFIG_SPLITS[name]:
+        out, lse = H.run_op(inp, split)
+        res = H.compare(out, lse, exp_out, exp_lse, rows=rows)
+        print(name, split, res, flush=True)
+
+
+# ------------------------------------------------------------ reference's own shapes
+# vllm-main-l20-paged-decode-rfc.patch:487-582 (upstream test), seed 17, D=128
+UPSTREAM = [(1, 129, 12, 2), (1, 2304, 16, 8), (4, 513, 12, 2), (4, 640, 16, 8)]
+
+
+@pytest.mark.parametrize("batch,ctx,hq,hkv", UPSTREAM)
+@pytest.mark.parametrize("split", [64, 128, 512])
+def test_reference_upstream_shapes(batch, ctx, hq, hkv, split):
+    inp = H.make_synthetic(batch, hq, hkv, 128, [ctx] * batch, seed=17)
+    exp = H.run_oracle(inp)
+    H.compare(*H.run_op(inp, split), *exp)
+
+
+# ------------------------------------------------------------ edge cases
+EDGE = [
+    # batch, hq, hkv, d, lens, q_len, per_head, dtype
+    ("ragged_d64", 5, 14, 2, 64, [1, 15, 16, 17, 500], 1, False, torch.bfloat16),
+    ("ragged_d128", 5, 28, 4, 128, [1, 15, 16, 33, 1025], 1, True, torch.bfloat16),
+    ("empty_seq", 3, 8, 2, 128, [0, 40, 0], 1, False, torch.bfloat16),
+    ("fp16_query", 2, 16, 2, 128, [300, 77], 1, False, torch.float16),
+    ("mha_g1", 2, 4, 4, 128, [200, 90], 1, False, torch.bfloat16),
+    ("group16", 2, 32, 2, 128, [129, 700], 1, False, torch.bfloat16),
+    ("verify_q4", 3, 16, 2, 128, [70, 4, 513], 4, False, torch.bfloat16),
+    ("verify_q4_short", 2, 8, 2, 64, [2, 3], 4, True, torch.bfloat16),
+    ("verify_q2_g16", 2, 32, 2, 128, [65, 300], 2, False, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", EDGE, ids=[e[0] for e in EDGE])
+@pytest.mark.parametrize("split", [64, 96, 1024])
+def test_edge_cases(case, split):
+    _, batch, hq, hkv, d, lens, q_len, per_head, dtype = case
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, per_head=per_head, dtype=dtype,
+                           seed=zlib.crc32(case[0].encode()) % 1000, garbage_tail=True)
+    exp = H.run_oracle(inp)
+    H.compare(*H.run_op(inp, split), *exp)
+
+
+def test_c_abi_and_torch_op_agree_bitwise():
+    inp = H.make_synthetic(3, 28, 4, 128, [900, 31, 4000], seed=5)
+    a = H.run_op(inp, 256, via="torch")
+    b = H.run_op(inp, 256, via="cabi")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    H.compare(*b, *H.run_oracle(inp))
+
+
+def test_fp16_partial_workspace():
+    inp = H.make_synthetic(2, 16, 2, 128, [1500, 700], seed=6)
+    H.compare(*H.run_op(inp, 128, partial_dtype=torch.float16), *H.run_oracle(inp))
+
+
+def test_strided_kv_views_like_vllm_unbind():
+    """vLLM's cache is [num_blocks, 2, 16, Hkv, D]; unbind(1) gives strided K/V views."""
+    inp = H.make_synthetic(3, 16, 8, 128, [100, 1000, 37], seed=7)
+    joint = torch.stack([inp["key_cache"], inp["value_cache"]], dim=1)  # [P, 2, 16, Hkv, D]
+    k_view, v_view = joint.unbind(1)
+    assert k_view.stride(0) == 2 * 16 * 8 * 128
+    out = H.run_op(inp, 128, key_cache=k_view, value_cache=v_view)
+    H.compare(*out, *H.run_oracle(inp))
+
+
+def test_split_size_invariance():
+    inp = H.make_synthetic(4, 28, 4, 128, [5000, 1234, 77, 2048], seed=8)
+    exp = H.run_oracle(inp)
+    outs = []
+    for split in (64, 128, 272, 512, 1024):
+        out, lse = H.run_op(inp, split)
+        H.compare(out, lse, *exp)
+        outs.append(out.float())
+    for o in outs[1:]:
+        assert float((o - outs[0]).abs().max()) <= 1e-2
+
+
+def test_hook_api_with_auto_split_and_reused_workspace():
+    import l20_paged_split_kv as sk
+
+    inp = H.make_synthetic(8, 16, 2, 128, [600, 2048, 31, 4096, 1, 300, 999, 2500], seed=9, per_head=True)
+    ws = sk.allocate_l20_paged_split_kv_workspace(inp["query"], inp["max_seq_len"], split_size=256)
+    exp = H.run_oracle(inp)
+    for _ in range(2):
+        lse = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+        out = sk.l20_paged_split_kv_attention_fp8(
+            inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
+            k_scale=inp["k_scale"], v_scale=inp["v_scale"], max_seq_len=inp["max_seq_len"], split_size=256,
+            workspace=ws, lse=lse)
+        torch.cuda.synchronize()
+        H.compare(out, lse, *exp)
+    out = sk.l20_paged_split_kv_attention_fp8(
+        inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
+        k_scale=inp["k_scale"], v_scale=inp["v_scale"], split_size=None)
+    torch.cuda.synchronize()
+    H.compare(out, None, exp[0], None, check_lse=False)
+
+
+def test_hip_graph_capture_replays_match_eager():
+    import l20_paged_decode  # noqa: F401
+
+    inp = H.make_synthetic(4, 28, 4, 128, [3000, 700, 64, 1500], seed=10)
+    po, pm, ps = H.workspace(inp, 256)
+    out = torch.empty_like(inp["query"])
+    lse = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+
+    def call():
+        torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
+            inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
+            po, pm, ps, out, inp["k_scale"], inp["v_scale"], inp["max_seq_len"], 256,
+            inp["softmax_scale"], None, None, 1, lse)
+
+    call()
+    torch.cuda.synchronize()
+    eager_out, eager_lse = out.clone(), lse.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        out.zero_()
+        lse.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out) and torch.equal(lse, eager_lse)

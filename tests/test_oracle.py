@@ -1,0 +1,287 @@
+"""Pins for the CPU oracle (oracle/paged_fp8_decode_ref.py), CPU only.
+
+Each oracle function is checked against something other than its own formula:
+torch's float8_e4m3fn conversion (a library routine), closed forms, the
+reference's masked-attention known answer, an independent float64 loop, and
+invariances.  The mutation tests at the end plant plausible mistakes in a copy
+of the oracle and show that the checks here catch them.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_fp8_decode_ref as ref
+
+
+# ---------------------------------------------------------------- fp8 codec
+def test_decode_table_matches_closed_form_and_torch():
+    table = ref.e4m3fn_decode_table()
+    codes = torch.arange(256, dtype=torch.uint8)
+    via_torch = codes.view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(table)
+    assert np.array_equal(np.flatnonzero(nan), [0x7F, 0xFF])
+    assert np.array_equal(np.isnan(via_torch), nan)
+    assert np.array_equal(table[~nan], via_torch[~nan])
+    # spot values of the OCP e4m3fn format
+    assert table[0x00] == 0.0 and table[0x80] == 0.0 and np.signbit(table[0x80])
+    assert table[0x01] == 2.0 ** -9          # smallest subnormal
+    assert table[0x08] == 2.0 ** -6          # smallest normal
+    assert table[0x38] == 1.0
+    assert table[0x7E] == 448.0 and table[0xFE] == -448.0
+
+
+def test_encode_matches_torch_rne_on_random_and_midpoints():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 50,
+        rng.uniform(-448, 448, 20000).astype(np.float32),
+        rng.standard_normal(5000).astype(np.float32) * 1e-3,
+    ])
+    pos = ref.e4m3fn_decode_table()[:0x7F].astype(np.float64)
+    mids = ((pos[1:] + pos[:-1]) / 2).astype(np.float32)
+    mids = mids[(mids.astype(np.float64) == (pos[1:] + pos[:-1]) / 2)]  # exact midpoints only
+    vals = np.concatenate([vals, mids, -mids, np.nextafter(mids, 0), np.nextafter(mids, 1000)])
+    vals = np.clip(vals, -448, 448)
+    ours = ref.encode_e4m3fn(vals)
+    theirs = torch.from_numpy(vals).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    # -0.0 vs +0.0 for values rounding to zero: compare decoded values and sign
+    assert np.array_equal(ref.e4m3fn_to_f32(ours), ref.e4m3fn_to_f32(theirs))
+    assert np.array_equal(ours, theirs)
+
+
+def test_quantize_matches_torch_workload_quantizer():
+    import l20_pd_workloads as wl
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(8, 16, 3, 64, generator=g).to(torch.bfloat16)
+    codes_t, scale_t = wl.quantize_fp8_e4m3(x)
+    codes_n, scale_n = ref.quantize_fp8_e4m3(x.float().numpy())
+    assert np.float32(scale_t) == np.float32(scale_n)
+    assert np.array_equal(codes_t.view(torch.uint8).numpy(), codes_n)
+    codes_t, scales_t = wl.quantize_fp8_e4m3(x, per_head_axis=2)
+    codes_n, scales_n = ref.quantize_fp8_e4m3_per_head(x.float().numpy(), head_axis=2)
+    assert np.array_equal(scales_t.numpy(), scales_n)
+    assert np.array_equal(codes_t.view(torch.uint8).numpy(), codes_n)
+
+
+# ---------------------------------------------------------------- helpers
+def make_case(seed, batch, hq, hkv, d, lens, q_len=1, per_head=False, pool_extra=3):
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int32)
+    pages_per = (lens + 15) // 16
+    pool = int(pages_per.sum()) + pool_extra
+    perm = rng.permutation(pool)
+    table = np.zeros((batch, max(1, int(pages_per.max()))), dtype=np.int32)
+    off = 0
+    for b in range(batch):
+        table[b, :pages_per[b]] = perm[off:off + pages_per[b]]
+        off += pages_per[b]
+    query = rng.standard_normal((batch * q_len, hq, d)).astype(np.float32)
+    k = rng.standard_normal((pool, 16, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((pool, 16, hkv, d)).astype(np.float32)
+    if per_head:
+        kc, ks = ref.quantize_fp8_e4m3_per_head(k)
+        vc, vs = ref.quantize_fp8_e4m3_per_head(v)
+    else:
+        kc, ks = ref.quantize_fp8_e4m3(k)
+        vc, vs = ref.quantize_fp8_e4m3(v)
+    return dict(query=query, key_cache=kc, value_cache=vc, block_table=table, seq_lens=lens,
+                k_scale=ks, v_scale=vs, q_len=q_len)
+
+
+def run(fn, case, **kw):
+    c = dict(case)
+    q_len = c.pop("q_len")
+    return fn(c["query"], c["key_cache"], c["value_cache"], c["block_table"], c["seq_lens"],
+              c["k_scale"], c["v_scale"], q_len=q_len, **kw)
+
+
+TINY = [
+    dict(seed=1, batch=2, hq=4, hkv=2, d=64, lens=[17, 33]),
+    dict(seed=2, batch=1, hq=3, hkv=1, d=128, lens=[40], per_head=False),
+    dict(seed=3, batch=2, hq=4, hkv=2, d=64, lens=[21, 9], q_len=4, per_head=True),
+    dict(seed=4, batch=1, hq=2, hkv=2, d=64, lens=[16], q_len=2),
+]
+
+
+@pytest.mark.parametrize("spec", TINY)
+def test_reference_matches_fp64_brute_force(spec):
+    case = make_case(**spec)
+    out, lse = run(ref.reference, case)
+    out64, lse64 = run(ref.brute_force_fp64, case)
+    np.testing.assert_allclose(out, out64, atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(lse, lse64, atol=2e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("spec", TINY)
+@pytest.mark.parametrize("split", [16, 32, 48])
+def test_split_reference_matches_reference(spec, split):
+    case = make_case(**spec)
+    out, lse = run(ref.reference, case, acc_dtype=np.float64)
+    out_s, lse_s = run(ref.split_reference, case, split_size=split)
+    np.testing.assert_allclose(out_s, out, atol=1e-6)
+    np.testing.assert_allclose(lse_s, lse, atol=1e-6)
+
+
+# ---------------------------------------------------------------- closed forms
+def _identity_case(d=64, length=48, hkv=1, hq=2):
+    pages = (length + 15) // 16
+    table = np.arange(pages, dtype=np.int32)[None]
+    return table, np.array([length], dtype=np.int32), pages
+
+
+def test_equal_keys_give_mean_of_values_and_lse_s_plus_log_l():
+    d, length = 64, 48
+    table, lens, pages = _identity_case(d, length)
+    rng = np.random.default_rng(7)
+    kc = np.full((pages, 16, 1, d), 0x38, dtype=np.uint8)           # every key element = 1.0
+    vc = ref.encode_e4m3fn(np.clip(rng.standard_normal((pages, 16, 1, d)) * 4, -448, 448)).reshape(pages, 16, 1, d)
+    q = rng.standard_normal((1, 2, d)).astype(np.float32)
+    out, lse = ref.reference(q, kc, vc, table, lens, 1.0, 0.5)
+    vals = ref.e4m3fn_to_f32(vc).reshape(-1, d)[:length] * 0.5
+    np.testing.assert_allclose(out[0, 0], vals.mean(axis=0), atol=1e-6)
+    s = q[0].sum(axis=1) * d ** -0.5                                 # q . 1 * scale
+    np.testing.assert_allclose(lse[0], s + math.log(length), rtol=1e-6)
+
+
+def test_single_token_returns_v0_and_dominant_score_selects_its_row():
+    d = 128
+    table, lens, pages = _identity_case(d, 1)
+    rng = np.random.default_rng(8)
+    kc = ref.encode_e4m3fn(np.clip(rng.standard_normal((pages, 16, 1, d)), -448, 448))
+    vc = ref.encode_e4m3fn(np.clip(rng.standard_normal((pages, 16, 1, d)), -448, 448))
+    q = rng.standard_normal((1, 1, d)).astype(np.float32)
+    out, _ = ref.reference(q, kc, vc, table, lens, 1.0, 2.0)
+    np.testing.assert_allclose(out[0, 0], ref.e4m3fn_to_f32(vc[0, 0, 0]) * 2.0, rtol=1e-6)
+    # one key aligned with a large query dominates the softmax
+    table, lens, pages = _identity_case(d, 32)
+    kc = np.zeros((pages, 16, 1, d), dtype=np.uint8)
+    kc[1, 3, 0, :] = 0x7E                                           # token 19 = 448 everywhere
+    q = np.ones((1, 1, d), dtype=np.float32)
+    vc = ref.encode_e4m3fn(np.clip(rng.standard_normal((pages, 16, 1, d)), -448, 448))
+    out, _ = ref.reference(q, kc, vc, table, lens, 1.0, 1.0)
+    np.testing.assert_allclose(out[0, 0], ref.e4m3fn_to_f32(vc[1, 3, 0]), rtol=1e-6)
+
+
+def test_reference_masked_attention_known_answer():
+    """tests/test_tree_attention.py:36-53 of the reference, restated for the chain mask.
+
+    Two draft rows over 2 cached + 2 draft keys; query = ones(2), keys
+    [1,0],[0,1],[2,0],[0,2], values 1,2,4,8 in dim 0, scale 2^-0.5.  With the
+    causal chain, row 0 sees keys 0..2 and row 1 sees keys 0..3.
+    """
+    d = 64  # pad the 2-dim example with zeros (no effect on scores or values)
+    k = np.zeros((1, 16, 1, d), dtype=np.float32)
+    v = np.zeros((1, 16, 1, d), dtype=np.float32)
+    k[0, 0, 0, 0], k[0, 1, 0, 1], k[0, 2, 0, 0], k[0, 3, 0, 1] = 1, 1, 2, 2
+    v[0, :4, 0, 0] = [1, 2, 4, 8]
+    kc, vc = ref.encode_e4m3fn(k), ref.encode_e4m3fn(v)
+    q = np.zeros((2, 1, d), dtype=np.float32)
+    q[:, 0, :2] = 1.0
+    out, _ = ref.reference(q, kc, vc, np.array([[0]], np.int32), np.array([4], np.int32), 1.0, 1.0,
+                           softmax_scale=2 ** -0.5, q_len=2)
+    a, b2 = math.exp(2 ** -0.5), math.exp(2 * 2 ** -0.5)
+    row0 = (1 * a + 2 * a + 4 * b2) / (a + a + b2)
+    row1 = (1 * a + 2 * a + 4 * b2 + 8 * b2) / (a + a + b2 + b2)
+    np.testing.assert_allclose(out[:, 0, 0], [row0, row1], rtol=1e-6)
+
+
+# ---------------------------------------------------------------- invariances
+def test_page_permutation_invariance():
+    case = make_case(11, 2, 4, 2, 64, [70, 35], pool_extra=10)
+    out, lse = run(ref.reference, case)
+    # move every page to a new physical slot
+    rng = np.random.default_rng(12)
+    pool = case["key_cache"].shape[0]
+    perm = rng.permutation(pool)
+    inv = np.argsort(perm)
+    moved = dict(case, key_cache=case["key_cache"][inv], value_cache=case["value_cache"][inv],
+                 block_table=perm[case["block_table"]].astype(np.int32))
+    out2, lse2 = run(ref.reference, moved)
+    np.testing.assert_array_equal(out, out2)
+    np.testing.assert_array_equal(lse, lse2)
+
+
+def test_gqa_equals_mha_with_replicated_heads():
+    case = make_case(13, 2, 6, 2, 64, [30, 50])
+    out, lse = run(ref.reference, case)
+    mha = dict(case, key_cache=np.repeat(case["key_cache"], 3, axis=2),
+               value_cache=np.repeat(case["value_cache"], 3, axis=2))
+    out2, lse2 = run(ref.reference, mha)
+    np.testing.assert_allclose(out, out2, atol=1e-6)
+    np.testing.assert_allclose(lse, lse2, atol=1e-6)
+
+
+def test_equal_per_head_scales_equal_per_tensor():
+    case = make_case(14, 1, 4, 2, 64, [45])
+    out, lse = run(ref.reference, case)
+    ph = dict(case, k_scale=np.full(2, case["k_scale"], np.float32), v_scale=np.full(2, case["v_scale"], np.float32))
+    out2, lse2 = run(ref.reference, ph)
+    np.testing.assert_array_equal(out, out2)
+    np.testing.assert_array_equal(lse, lse2)
+
+
+def test_causal_row_equals_single_query_on_shortened_sequence():
+    q_len = 4
+    case = make_case(15, 2, 4, 2, 64, [37, 20], q_len=q_len)
+    out, lse = run(ref.reference, case)
+    for i in range(q_len):
+        rows = np.arange(2) * q_len + i
+        single = dict(case, query=case["query"][rows], q_len=1,
+                      seq_lens=case["seq_lens"] - (q_len - 1 - i))
+        o1, l1 = run(ref.reference, single)
+        np.testing.assert_allclose(out[rows], o1, atol=1e-6)
+        np.testing.assert_allclose(lse[rows], l1, atol=1e-6)
+
+
+def test_empty_rows_give_zero_and_minus_inf():
+    case = make_case(16, 2, 2, 1, 64, [0, 2], q_len=3)
+    out, lse = run(ref.reference, case)
+    assert np.all(out[:3] == 0) and np.all(np.isneginf(lse[:3]))     # L = 0
+    assert np.all(out[3] == 0) and np.all(np.isneginf(lse[3]))       # row 0 of L=2 sees nothing
+    assert np.all(np.isfinite(lse[4:]))
+    out64, lse64 = run(ref.brute_force_fp64, case)
+    np.testing.assert_allclose(out, out64, atol=2e-6)
+
+
+# ---------------------------------------------------------------- planted mistakes
+def _mutant(kind):
+    """A copy of ``ref.reference`` with one plausible bug planted."""
+
+    def mutant(query, key_cache, value_cache, block_table, seq_lens, k_scale, v_scale, *, q_len=1, **kw):
+        if kind == "causal_off_by_one":
+            seq_lens = np.asarray(seq_lens) - 1
+            out, lse = ref.reference(query, key_cache, value_cache, block_table, seq_lens, k_scale, v_scale,
+                                     q_len=q_len, **kw)
+            return out, lse
+        if kind == "head_modulo":   # kv head = h % Hkv instead of h // G
+            hkv = key_cache.shape[2]
+            g = query.shape[1] // hkv
+            order = np.array([(h % hkv) * g + h // hkv for h in range(query.shape[1])])
+            out, lse = ref.reference(query[:, order], key_cache, value_cache, block_table, seq_lens, k_scale,
+                                     v_scale, q_len=q_len, **kw)
+            inv = np.argsort(order)
+            return out[:, inv], lse[:, inv]
+        if kind == "no_v_scale":
+            return ref.reference(query, key_cache, value_cache, block_table, seq_lens, k_scale, 1.0,
+                                 q_len=q_len, **kw)
+        if kind == "page_slot_swapped":  # token -> (t % 16, t // 16)
+            kc = np.swapaxes(key_cache, 0, 1).copy() if key_cache.shape[0] == 16 else key_cache[:, ::-1]
+            vc = np.swapaxes(value_cache, 0, 1).copy() if value_cache.shape[0] == 16 else value_cache[:, ::-1]
+            return ref.reference(query, kc, vc, block_table, seq_lens, k_scale, v_scale, q_len=q_len, **kw)
+        raise ValueError(kind)
+
+    return mutant
+
+
+@pytest.mark.parametrize("kind", ["causal_off_by_one", "head_modulo", "no_v_scale", "page_slot_swapped"])
+def test_planted_mistakes_are_caught_by_brute_force(kind):
+    case = make_case(21, 2, 4, 2, 64, [23, 31], q_len=2)
+    if kind == "no_v_scale":
+        case["v_scale"] = 0.37
+    good, _ = run(ref.brute_force_fp64, case)
+    bad, _ = run(_mutant(kind), case)
+    assert not np.allclose(bad, good, atol=1e-3)
