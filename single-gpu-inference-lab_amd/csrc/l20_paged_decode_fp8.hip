@@ -94,23 +94,27 @@ template <typename QT> struct MfmaTypes;
 template <> struct MfmaTypes<__bf16> { typedef bf16x8 vec8; };
 template <> struct MfmaTypes<_Float16> { typedef f16x8 vec8; };
 
-// Four e4m3fn codes (one dword) -> four bf16 (exact: every e4m3fn value is a
-// bf16 value).  gfx950 v_cvt_scalef32_pk_bf16_fp8 with scale 1.0.
-__device__ __forceinline__ void fp8x4_to(bf16x8 &dst, int slot, int w) {
-  bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
-  bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
-  dst[slot + 0] = lo[0];
-  dst[slot + 1] = lo[1];
-  dst[slot + 2] = hi[0];
-  dst[slot + 3] = hi[1];
+// Eight e4m3fn codes (two dwords) -> eight bf16 / f16 MFMA operand elements,
+// exact (every e4m3fn value is representable in both).  gfx950
+// v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1.0, word_sel picking bytes
+// 0-1 or 2-3.  The pairs are moved as whole 32-bit words: per-lane extraction
+// of these conversions' results is miscompiled by the ROCm 7.2 LLVM.
+template <typename V8> __device__ __forceinline__ V8 fp8x8_to(int w0, int w1);
+template <> __device__ __forceinline__ bf16x8 fp8x8_to<bf16x8>(int w0, int w1) {
+  const i32x4 r = {
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+  return __builtin_bit_cast(bf16x8, r);
 }
-__device__ __forceinline__ void fp8x4_to(f16x8 &dst, int slot, int w) {
-  f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
-  f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
-  dst[slot + 0] = lo[0];
-  dst[slot + 1] = lo[1];
-  dst[slot + 2] = hi[0];
-  dst[slot + 3] = hi[1];
+template <> __device__ __forceinline__ f16x8 fp8x8_to<f16x8>(int w0, int w1) {
+  const i32x4 r = {
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+  return __builtin_bit_cast(f16x8, r);
 }
 
 __device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
@@ -312,9 +316,7 @@ __global__ __launch_bounds__(256) void pd_fp8_partial(PartialParams p) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const i32x4 raw = r.k[T][s >> 1];
-        qvec8 kop;
-        fp8x4_to(kop, 0, raw[2 * (s & 1)]);
-        fp8x4_to(kop, 4, raw[2 * (s & 1) + 1]);
+        const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
 #pragma unroll
         for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
       }
@@ -559,27 +561,45 @@ __global__ __launch_bounds__(256) void pd_merge(MergeParams p) {
 // ---------------------------------------------------------------------------
 // Bulk dequantisers (same conversions as the attention kernel)
 // ---------------------------------------------------------------------------
+// Four consecutive codes starting at i as one dword (zero-filled past n).
+__device__ __forceinline__ int load_codes4(const uint8_t *src, int64_t i, int64_t n) {
+  if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(src) + i) & 3) == 0)
+    return *reinterpret_cast<const int *>(src + i);
+  int w = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (i + e < n) w |= (int)src[i + e] << (8 * e);
+  return w;
+}
+
 __global__ void dequant_f32_kernel(const uint8_t *src, float *dst, int64_t n, float scale) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
-  int w = 0;
-  const int cnt = (n - i) < 4 ? (int)(n - i) : 4;
-  for (int e = 0; e < cnt; ++e) w |= (int)src[i + e] << (8 * e);
+  const int w = load_codes4(src, i, n);
   const f32x2 lo = fp8x2_f32(w, false);
   const f32x2 hi = fp8x2_f32(w, true);
   const float v[4] = {lo[0], lo[1], hi[0], hi[1]};
-  for (int e = 0; e < cnt; ++e) dst[i + e] = v[e] * scale;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (i + e < n) dst[i + e] = v[e] * scale;
 }
 
 __global__ void dequant_bf16_kernel(const uint8_t *src, uint16_t *dst, int64_t n) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
-  int w = 0;
-  const int cnt = (n - i) < 4 ? (int)(n - i) : 4;
-  for (int e = 0; e < cnt; ++e) w |= (int)src[i + e] << (8 * e);
-  bf16x8 v;
-  fp8x4_to(v, 0, w);
-  for (int e = 0; e < cnt; ++e) dst[i + e] = __builtin_bit_cast(uint16_t, v[e]);
+  const int w = load_codes4(src, i, n);
+  // Same conversion as the attention kernel's K operand; words, not lanes.
+  const i32x4 both = __builtin_bit_cast(i32x4, fp8x8_to<bf16x8>(w, 0));
+  const uint32_t lo = (uint32_t)both[0];
+  const uint32_t hi = (uint32_t)both[1];
+  if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(dst + i) & 7) == 0)) {
+    *reinterpret_cast<i32x2 *>(dst + i) = i32x2{(int)lo, (int)hi};
+    return;
+  }
+  const uint32_t words[2] = {lo, hi};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (i + e < n) dst[i + e] = (uint16_t)(words[e >> 1] >> (16 * (e & 1)));
 }
 
 }  // namespace l20pd
