@@ -2,7 +2,7 @@
 //
 // Two kernels per call, both enqueued on the caller's stream:
 //
-//  pd_fp8_partial<QT, D, NQT>   grid (num_splits, num_kv_heads, batch), 1-4 waves.
+//  pd_fp8_partial<QT, D, NQT>   grid (num_kv_heads, batch, num_splits), 1-4 waves.
 //    One workgroup owns one (sequence, KV head, split) work item and computes
 //    attention for ALL query rows of that KV head (GQA group x q_len, padded to
 //    16 * NQT MFMA columns), so each K/V page is read from HBM exactly once.
@@ -171,9 +171,13 @@ __global__ __launch_bounds__(256) void pd_fp8_partial(PartialParams p) {
   __shared__ float sm_m[kMaxWaves][16];
   __shared__ float sm_l[kMaxWaves][16];
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  // Grid (kv_head, batch, split): the hardware deals consecutive workgroup ids
+  // round-robin to the 8 XCDs, so the fastest dimension must spread work
+  // evenly -- with split fastest, every XCD would get one split index and
+  // XCD 0 all the split-0 work.  Empty splits also dispatch last this way.
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
   const int L = min(p.seq_lens[b], p.l_cap);
   const int split_start = split * p.split_size;
   if (split_start >= L) {  // uniform: nothing in this split
@@ -633,6 +637,8 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (a->split_size < 64 || a->split_size > 1024 || a->split_size % 16 != 0)
     return fail(L20_PD_EINVAL, "split_size must be a multiple of 16 from 64 through 1024");
   if (a->batch < 0 || a->max_seq_len < 0) return fail(L20_PD_EINVAL, "batch and max_seq_len must be >= 0");
+  if (a->batch > 65535 || l20_pd_num_splits(a->max_seq_len, a->split_size) > 65535)
+    return fail(L20_PD_EINVAL, "batch and the split count must be at most 65535");
   if (a->batch == 0) return L20_PD_OK;
   if (!a->query || !a->key_cache || !a->value_cache || !a->block_table || !a->seq_lens || !a->output)
     return fail(L20_PD_EINVAL, "null tensor pointer");
@@ -667,7 +673,7 @@ int32_t check_args(const l20_pd_fp8_args *a) {
 template <typename QT, int D, int NQT>
 hipError_t launch_partial(const l20pd::PartialParams &pp, int batch, int num_kv_heads, int nwaves,
                           hipStream_t stream) {
-  dim3 grid(pp.num_splits, num_kv_heads, batch);
+  dim3 grid(num_kv_heads, batch, pp.num_splits);
   hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), grid, dim3(64 * nwaves), 0, stream, pp);
   return hipGetLastError();
 }
