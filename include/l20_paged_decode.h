@@ -151,6 +151,16 @@ int32_t l20_pd_fp8_e4m3_dequant_f32(const uint8_t *src, float *dst, int64_t n,
 int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst,
                                      int64_t n, void *stream);
 
+/* HBM calibration (no reference counterpart; measurement support).
+ * stream_read reads `bytes` once with 16-byte nontemporal loads over
+ * `blocks` workgroups of 256 threads (sink: int32 [blocks], practically never
+ * written); stream_copy copies `bytes` from src to dst.  Used to measure the
+ * device's read ceiling and to scale FETCH_SIZE / WRITE_SIZE counters. */
+int32_t l20_pd_stream_read(const void *src, int64_t bytes, int32_t *sink,
+                           int32_t blocks, void *stream);
+int32_t l20_pd_stream_copy(const void *src, void *dst, int64_t bytes,
+                           int32_t blocks, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,17 +53,23 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPage = 16;
-constexpr int kMaxWaves = 4;
+constexpr int kMaxWaves = 8;       // waves per partial workgroup (one per KV head)
+constexpr int kMaxCompactBatch = 8192;  // sequences whose work list fits in LDS
+constexpr int kDepth = 2;               // K/V blocks in flight per wave
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: dword 3 (format bits)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleLog2 = 8.0f;  // lazy online-softmax rescale threshold (log2 units)
 
 struct PartialParams {
   const void *q;
   int64_t q_srow, q_shead;
   const uint8_t *k;
-  int64_t k_spage, k_stok, k_shead;
+  int64_t k_spage;
+  int k_stok32, k_shead32, k_extent;
   const uint8_t *v;
-  int64_t v_spage, v_stok, v_shead;
+  int64_t v_spage;
+  int v_stok32, v_shead32, v_extent;
   const int32_t *bt;
   int64_t bt_srow;
   const int32_t *seq_lens;
@@ -85,6 +91,7 @@ struct PartialParams {
   int q_len, num_q_heads, num_kv_heads, group, split_size, num_splits;
   int po_f32;
   int l_cap;  // min(num_splits * split_size, block-table pages * 16): tokens past it are never touched
+  int batch;
 };
 
 // ---------------------------------------------------------------------------
@@ -158,320 +165,403 @@ template <> struct BlockRaw<64> {
 // ---------------------------------------------------------------------------
 // Partial kernel
 // ---------------------------------------------------------------------------
-template <typename QT, int D, int NQT>
-__global__ __launch_bounds__(256) void pd_fp8_partial(PartialParams p) {
-  typedef typename MfmaTypes<QT>::vec8 qvec8;
-  constexpr int NCH = D / 64;        // 64-byte K chunks per token row
-  constexpr int NS = 2 * NCH;        // 32-wide k slices of the QK product
-  constexpr int NT = D / 16;         // 16-row d tiles of the PV product
-  constexpr int DPL = D / 4;         // contiguous output dims per lane
-  constexpr int LDS_STRIDE = D + 4;  // padded row of the LDS combine buffer
+// Two fp32 -> packed 16-bit words (bf16 or f16, round to nearest even).
+template <typename QT> __device__ __forceinline__ int pack2(float a, float b);
+template <> __device__ __forceinline__ int pack2<__bf16>(float a, float b) {
+  return __builtin_bit_cast(int, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <> __device__ __forceinline__ int pack2<_Float16>(float a, float b) {
+  return __builtin_bit_cast(int, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
 
-  __shared__ float sm_o[kMaxWaves][16][LDS_STRIDE];
-  __shared__ float sm_m[kMaxWaves][16];
-  __shared__ float sm_l[kMaxWaves][16];
-
-  // Grid (kv_head, batch, split): the hardware deals consecutive workgroup ids
-  // round-robin to the 8 XCDs, so the fastest dimension must spread work
-  // evenly -- with split fastest, every XCD would get one split index and
-  // XCD 0 all the split-0 work.  Empty splits also dispatch last this way.
-  const int kvh = blockIdx.x;
-  const int b = blockIdx.y;
-  const int split = blockIdx.z;
+// Splits of sequence b: ceil(L / split_size), and one (zero-writing) item
+// for an empty sequence.
+__device__ __forceinline__ int splits_of(const PartialParams &p, int b) {
   const int L = min(p.seq_lens[b], p.l_cap);
-  const int split_start = split * p.split_size;
-  if (split_start >= L) {  // uniform: nothing in this split
-    if (split == 0) {
-      // Empty sequence: zero output and -inf LSE for all its query rows.
-      const int rows = p.group * p.q_len;
-      for (int idx = threadIdx.x; idx < rows * D; idx += blockDim.x) {
-        const int col = idx / D;
-        const int d = idx - col * D;
-        const int g = col / p.q_len;
-        const int i = col - g * p.q_len;
-        const int64_t row = (int64_t)b * p.q_len + i;
-        const int64_t h = (int64_t)kvh * p.group + g;
-        reinterpret_cast<QT *>(p.out)[row * p.o_srow + h * p.o_shead + d] = from_f32<QT>(0.0f);
-        if (d == 0 && p.lse) p.lse[row * p.lse_srow + h * p.lse_shead] = -INFINITY;
-      }
-    }
-    return;
+  return L > 0 ? (L + p.split_size - 1) / p.split_size : 1;
+}
+
+// Inclusive scan of one value per thread over the workgroup (<= 512 threads).
+__device__ __forceinline__ int block_inclusive_scan(int v, int *s_wave) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(v, off);
+    if (lane >= off) v += t;
   }
-  const int n_splits_b = (L + p.split_size - 1) / p.split_size;
-  const int split_end = min(split_start + p.split_size, L);
-  const bool direct = (n_splits_b == 1);
+  if (lane == 63) s_wave[wave] = v;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_wave[w];
+  __syncthreads();
+  return v + base;
+}
+
+// Persistent, page-major partial kernel.
+//
+// Work items are the (sequence, split) pairs, numbered sequence-major in a
+// compact list built at kernel start from seq_lens (no empty items).  The
+// grid is sized to the machine; workgroup w takes items w, w + grid, ... so
+// consecutive items land on different XCDs and every workgroup gets the same
+// number of items.  Inside a workgroup, wave w owns KV heads w, w + W, ...:
+// the waves of one item read the interleaved per-head pieces of the same
+// 16-token pages at the same time, so the NHD page is fetched as a whole.
+template <typename QT, int D, int NQT>
+__global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
+  typedef typename MfmaTypes<QT>::vec8 qvec8;
+  constexpr int NCH = D / 64;  // 64-byte K chunks per token row
+  constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
+  constexpr int NT = D / 16;   // 16-row d tiles of the PV product
+  constexpr int DPL = D / 4;   // contiguous output dims per lane
+
+  __shared__ int s_prefix[kMaxCompactBatch + 1];
+  __shared__ int s_wave[8];
 
   const int nwaves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int n16 = lane & 15;
   const int j = lane >> 4;
   const int q_len = p.q_len;
   const int mcols = p.group * q_len;
+  const int B = p.batch;
 
-  const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
-  const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
-  const float c_log2 = k_scale * p.qk_scale_log2;
+  // ---- compact work list: s_prefix[b] = first item of sequence b ----
+  const bool compact = B <= kMaxCompactBatch;
+  int total;
+  if (compact) {
+    int carry = 0;
+    if (threadIdx.x == 0) s_prefix[0] = 0;
+    for (int base = 0; base < B; base += blockDim.x) {
+      const int b = base + threadIdx.x;
+      const int n = b < B ? splits_of(p, b) : 0;
+      const int incl = block_inclusive_scan(n, s_wave);
+      if (b < B) s_prefix[b + 1] = carry + incl;
+      __syncthreads();
+      carry = s_prefix[min(base + (int)blockDim.x, B)];
+    }
+    total = __builtin_amdgcn_readfirstlane(s_prefix[B]);
+  } else {
+    total = B * p.num_splits;
+  }
 
-  // ---- query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16 ----
-  qvec8 qop[NQT][NS];
-  int lim[NQT];  // last visible token for this lane's column
-#pragma unroll
-  for (int qt = 0; qt < NQT; ++qt) {
-    const int col = 16 * qt + n16;
-    const int g = col / q_len;
-    const int i = col - g * q_len;
-    lim[qt] = min(split_end - 1, L - q_len + i);
-    if (col < mcols) {
-      const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
-                       (int64_t)(kvh * p.group + g) * p.q_shead;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
-        qop[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    int b, split;
+    if (compact) {
+      int lo = 0, hi = B - 1;  // last b with s_prefix[b] <= item
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (__builtin_amdgcn_readfirstlane(s_prefix[mid]) <= item)
+          lo = mid;
+        else
+          hi = mid - 1;
       }
+      b = lo;
+      split = item - __builtin_amdgcn_readfirstlane(s_prefix[b]);
     } else {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) qop[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
+      b = item / p.num_splits;
+      split = item - b * p.num_splits;
+      if (split >= splits_of(p, b)) continue;  // uniform over the workgroup
     }
-  }
-  int min_lim = min(split_end - 1, L - q_len);
+    const int L = min(p.seq_lens[b], p.l_cap);
 
-  // ---- page ids of this wave's blocks: lane e -> (block e/2, tile e%2) ----
-  const int tiles = (split_end - split_start + kPage - 1) / kPage;
-  const int nblk = (tiles + 1) >> 1;
-  int pid = -1;
-  {
-    const int ti = 2 * (wave + nwaves * (lane >> 1)) + (lane & 1);
-    if (ti < tiles) {
-      const int v = p.bt[(int64_t)b * p.bt_srow + split_start / kPage + ti];
-      pid = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
-    }
-  }
+    for (int kvh = wave; kvh < p.num_kv_heads; kvh += nwaves) {
+      if (L <= 0) {
+        // Empty sequence: zero output and -inf LSE for this head's rows.
+        for (int idx = lane; idx < mcols * D; idx += 64) {
+          const int col = idx / D;
+          const int d = idx - col * D;
+          const int g = col / q_len;
+          const int i = col - g * q_len;
+          const int64_t row = (int64_t)b * q_len + i;
+          const int64_t h = (int64_t)kvh * p.group + g;
+          reinterpret_cast<QT *>(p.out)[row * p.o_srow + h * p.o_shead + d] = from_f32<QT>(0.0f);
+          if (d == 0 && p.lse) p.lse[row * p.lse_srow + h * p.lse_shead] = -INFINITY;
+        }
+        continue;
+      }
+      const int split_start = split * p.split_size;
+      const int split_end = min(split_start + p.split_size, L);
+      const bool direct = (L + p.split_size - 1) / p.split_size == 1;
 
-  const int64_t koff = (int64_t)n16 * p.k_stok + (int64_t)kvh * p.k_shead + 16 * j;
-  const int64_t voff = (int64_t)(4 * j) * p.v_stok + (int64_t)kvh * p.v_shead + (D / 16) * n16;
+      const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
+      const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
+      const float c_log2 = k_scale * p.qk_scale_log2;
 
-  f32x4 acc[NQT][NT];
-  float m_run[NQT], l_run[NQT];
-#pragma unroll
-  for (int qt = 0; qt < NQT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.0f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  auto load_block = [&](BlockRaw<D> &r, int it) {
-#pragma unroll
-    for (int T = 0; T < 2; ++T) {
-      const int page = __builtin_amdgcn_readlane(pid, 2 * it + T);
-      if (page >= 0) {
-        const uint8_t *kp = p.k + (int64_t)page * p.k_spage + koff;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) r.k[T][c] = *reinterpret_cast<const i32x4 *>(kp + 64 * c);
-        const uint8_t *vp = p.v + (int64_t)page * p.v_spage + voff;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (D == 128)
-            r.v[4 * T + e] = *reinterpret_cast<const i32x2 *>(vp + e * p.v_stok);
-          else
-            r.v[4 * T + e] = *reinterpret_cast<const int *>(vp + e * p.v_stok);
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) r.k[T][c] = i32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (D == 128)
-            r.v[4 * T + e] = i32x2{0, 0};
-          else
-            r.v[4 * T + e] = 0;
-        }
-      }
-    }
-  };
-
-  auto compute_block = [&](BlockRaw<D> &r, int blk) {
-    const int tok0 = split_start + 32 * blk;
-    // Tokens past the end of the sequence may hold arbitrary bytes (NaN
-    // codes included): zero their V so that p = 0 contributes exactly 0.
-    if (tok0 + 32 > L) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-        if (t >= L) {
-          if constexpr (D == 128)
-            r.v[e] = i32x2{0, 0};
-          else
-            r.v[e] = 0;
-        }
-      }
-    }
-    // ---- S^T = K . Q^T ----
-    f32x4 sc[NQT][2];
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-      sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int T = 0; T < 2; ++T) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const i32x4 raw = r.k[T][s >> 1];
-        const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
-      }
-    }
-    // ---- online softmax (log2 domain) ----
-    const bool need_mask = (tok0 + 31 > min_lim);
-    f16x8 pop[NQT];
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = sc[qt][e >> 2][e & 3] * c_log2;
-      if (need_mask) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-          x[e] = (t <= lim[qt]) ? x[e] : -INFINITY;
-        }
-      }
-      float mloc = x[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
-      mloc = wave_max_xor16_32(mloc);
-      const float m_new = fmaxf(m_run[qt], mloc);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
-      float psum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(x[e] - m_use);
-        const float p1 = __builtin_amdgcn_exp2f(x[e + 1] - m_use);
-        psum += p0 + p1;
-        const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
-        pop[qt][e] = h[0];
-        pop[qt][e + 1] = h[1];
-      }
-      l_run[qt] = l_run[qt] * alpha + psum;
-      m_run[qt] = m_new;
-      if (__any(alpha != 1.0f)) {  // wave-uniform skip once the maxima settle
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[qt][t] *= alpha;
-      }
-    }
-    // ---- O^T += V^T . P^T ----
-#pragma unroll
-    for (int tp = 0; tp < NT; tp += 2) {
-      // d tiles tp, tp+1 use byte pair (tp % 4, tp % 4 + 1) of dword tp / 4
-      f16x8 va, vb;
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        int w0, w1;
-        if constexpr (D == 128) {
-          w0 = r.v[e][tp >> 2];
-          w1 = r.v[e + 1][tp >> 2];
-        } else {
-          w0 = r.v[e];
-          w1 = r.v[e + 1];
-        }
-        const f32x2 f0 = fp8x2_f32(w0, (tp & 3) != 0);
-        const f32x2 f1 = fp8x2_f32(w1, (tp & 3) != 0);
-        const f16x2 ha = __builtin_convertvector(f32x2{f0[0], f1[0]}, f16x2);
-        const f16x2 hb = __builtin_convertvector(f32x2{f0[1], f1[1]}, f16x2);
-        va[e] = ha[0];
-        va[e + 1] = ha[1];
-        vb[e] = hb[0];
-        vb[e + 1] = hb[1];
-      }
+      // ---- query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16 ----
+      qvec8 qop[NQT][NS];
+      int lim[NQT];  // last visible token for this lane's column
 #pragma unroll
       for (int qt = 0; qt < NQT; ++qt) {
-        acc[qt][tp] = mfma16(va, pop[qt], acc[qt][tp]);
-        acc[qt][tp + 1] = mfma16(vb, pop[qt], acc[qt][tp + 1]);
-      }
-    }
-  };
-
-  // ---- main loop: this wave's blocks blk = wave, wave + nwaves, ... ----
-  {
-    BlockRaw<D> cur, nxt;
-    int it = 0;
-    int blk = wave;
-    if (blk < nblk) load_block(cur, 0);
-    for (; blk < nblk; blk += nwaves, ++it) {
-      if (blk + nwaves < nblk) load_block(nxt, it + 1);
-      compute_block(cur, blk);
-      cur = nxt;
-    }
-  }
-
-  // ---- combine the waves through LDS, one 16-column query tile at a time ----
-  constexpr int D4 = D / 4;
+        const int col = 16 * qt + n16;
+        const int g = col / q_len;
+        const int i = col - g * q_len;
+        lim[qt] = min(split_end - 1, L - q_len + i);
+        if (col < mcols) {
+          const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
+                           (int64_t)(kvh * p.group + g) * p.q_shead;
 #pragma unroll
-  for (int qt = 0; qt < NQT; ++qt) {
-    const float l_tot = wave_sum_xor16_32(l_run[qt]);
-    if (qt > 0) __syncthreads();  // previous tile's readers are done
-    if (j == 0) {
-      sm_m[wave][n16] = m_run[qt];
-      sm_l[wave][n16] = l_tot;
-    }
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) sm_o[wave][n16][DPL * j + rr * NT + t] = acc[qt][t][rr];
-    }
-    __syncthreads();
-    const int tile_cols = min(16, mcols - 16 * qt);
-    const int total = tile_cols * D4;
-    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-      const int c16 = idx / D4;
-      const int d = 4 * (idx - c16 * D4);
-      float mm = -INFINITY;
-      for (int w = 0; w < nwaves; ++w) mm = fmaxf(mm, sm_m[w][c16]);
-      const float msafe = (mm == -INFINITY) ? 0.0f : mm;
-      float lsum = 0.0f;
-      f32x4 o = {0.f, 0.f, 0.f, 0.f};
-      for (int w = 0; w < nwaves; ++w) {
-        const float wt = __builtin_amdgcn_exp2f(sm_m[w][c16] - msafe);
-        lsum += wt * sm_l[w][c16];
-        o += wt * *reinterpret_cast<const f32x4 *>(&sm_o[w][c16][d]);
-      }
-      const float inv = (lsum > 0.0f) ? v_scale / lsum : 0.0f;
-      o *= inv;
-      const int col = 16 * qt + c16;
-      const int g = col / q_len;
-      const int i = col - g * q_len;
-      const int64_t row = (int64_t)b * q_len + i;
-      const int64_t h = (int64_t)kvh * p.group + g;
-      if (direct) {
-        QT *dst = reinterpret_cast<QT *>(p.out) + row * p.o_srow + h * p.o_shead + d;
-        dst[0] = from_f32<QT>(o[0]);
-        dst[1] = from_f32<QT>(o[1]);
-        dst[2] = from_f32<QT>(o[2]);
-        dst[3] = from_f32<QT>(o[3]);
-        if (d == 0 && p.lse) {
-          // v_log_f32 is log2
-          p.lse[row * p.lse_srow + h * p.lse_shead] =
-              (lsum > 0.0f) ? kLn2 * (msafe + __builtin_amdgcn_logf(lsum)) : -INFINITY;
-        }
-      } else {
-        const int64_t po_idx = row * p.po_srow + h * p.po_shead + (int64_t)split * p.po_ssplit + d;
-        if (p.po_f32) {
-          *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.po) + po_idx) = o;
+          for (int s = 0; s < NS; ++s) {
+            const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
+            qop[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
+          }
         } else {
-          _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx;
-          dst[0] = (_Float16)o[0];
-          dst[1] = (_Float16)o[1];
-          dst[2] = (_Float16)o[2];
-          dst[3] = (_Float16)o[3];
+#pragma unroll
+          for (int s = 0; s < NS; ++s) qop[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
         }
-        if (d == 0) {
-          p.pm[row * p.pm_srow + h * p.pm_shead + (int64_t)split * p.pm_ssplit] = mm;
-          p.pl[row * p.pl_srow + h * p.pl_shead + (int64_t)split * p.pl_ssplit] = lsum;
+      }
+      const int min_lim = min(split_end - 1, L - q_len);
+
+      // ---- page ids of the split: lane t -> tile t (a split has <= 64 tiles) ----
+      const int tiles = (split_end - split_start + kPage - 1) / kPage;
+      const int nblk = (tiles + 1) >> 1;
+      int pid = -1;
+      if (lane < tiles) {
+        const int v = p.bt[(int64_t)b * p.bt_srow + split_start / kPage + lane];
+        pid = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
+      }
+
+      // Lane offsets inside a page fit in 32 bits (checked on the host), so the
+      // loads take the (uniform 64-bit page base + 32-bit lane offset) form.
+      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
+      const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
+
+      f32x4 acc[NQT][NT];
+      float m_run[NQT], l_run[NQT];
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        m_run[qt] = -INFINITY;
+        l_run[qt] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+
+      // Raw buffer loads through a per-page resource: the page base lives in
+      // SGPRs, one 32-bit lane offset serves every K (V) load of the page and
+      // the hardware range check (the page's byte extent) returns zeros for
+      // anything outside it.  Loads are unconditional -- an invalid page id
+      // reads page 0 -- and compute_block zeroes V of every token outside
+      // the split or on an invalid page.
+      auto load_block = [&](BlockRaw<D> &r, int blk) {
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+          const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
+          const int page = raw_page >= 0 ? raw_page : 0;
+          const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, 0));
+          const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (D == 128)
+              r.v[4 * T + e] =
+                  __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, 0));
+            else
+              r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, 0);
+          }
+        }
+      };
+
+      auto compute_block = [&](BlockRaw<D> &r, int blk) {
+        const int tok0 = split_start + 32 * blk;
+        // Tokens past the split (the tail of the sequence's last page, or a
+        // tile beyond the split read from page 0) and tokens of an invalid
+        // page may hold arbitrary bytes, NaN codes included: zero their V so
+        // that p = 0 contributes exactly 0.  K needs no fix-up: their scores
+        // are replaced by -inf below.
+        const bool bad0 = __builtin_amdgcn_readlane(pid, 2 * blk) < 0;
+        const bool bad1 = __builtin_amdgcn_readlane(pid, 2 * blk + 1) < 0;
+        if (tok0 + 32 > split_end || bad0 || bad1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+            if (t >= split_end || ((e >> 2) ? bad1 : bad0)) {
+              if constexpr (D == 128)
+                r.v[e] = i32x2{0, 0};
+              else
+                r.v[e] = 0;
+            }
+          }
+        }
+        // ---- S^T = K . Q^T ----
+        f32x4 sc[NQT][2];
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+          sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+          sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const i32x4 raw = r.k[T][s >> 1];
+            const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
+          }
+        }
+        // ---- online softmax (log2 domain) ----
+        const bool need_mask = (tok0 + 31 > min_lim) || bad0 || bad1;
+        f16x8 pop[NQT];
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = sc[qt][e >> 2][e & 3] * c_log2;
+          if (need_mask) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+              x[e] = (t <= lim[qt] && !((e >> 2) ? bad1 : bad0)) ? x[e] : -INFINITY;
+            }
+          }
+          float mloc = x[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
+          mloc = wave_max_xor16_32(mloc);
+          // Lazy rescale: the reference max m_run only moves when some
+          // column's block max exceeds it by more than kRescaleLog2 (or it is
+          // still -inf).  P and l always use the same m_run, so the result is
+          // exact up to rounding; p stays below 2^kRescaleLog2 (f16 range).
+          if (__any(mloc > m_run[qt] + kRescaleLog2)) {
+            const float m_new = fmaxf(m_run[qt], mloc);
+            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
+            l_run[qt] *= alpha;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[qt][t] *= alpha;
+            m_run[qt] = m_new;
+          }
+          const float m_use = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
+          float psum = 0.0f;
+          i32x4 pw;
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(x[e] - m_use);
+            const float p1 = __builtin_amdgcn_exp2f(x[e + 1] - m_use);
+            psum += p0 + p1;
+            pw[e >> 1] = pack2<_Float16>(p0, p1);
+          }
+          pop[qt] = __builtin_bit_cast(f16x8, pw);
+          l_run[qt] += psum;
+        }
+        // ---- O^T += V^T . P^T ----
+#pragma unroll
+        for (int tp = 0; tp < NT; tp += 2) {
+          // d tiles tp, tp+1 use byte pair (tp % 4, tp % 4 + 1) of dword tp / 4
+          i32x4 wa, wb;
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            int w0, w1;
+            if constexpr (D == 128) {
+              w0 = r.v[e][tp >> 2];
+              w1 = r.v[e + 1][tp >> 2];
+            } else {
+              w0 = r.v[e];
+              w1 = r.v[e + 1];
+            }
+            const f32x2 f0 = fp8x2_f32(w0, (tp & 3) != 0);
+            const f32x2 f1 = fp8x2_f32(w1, (tp & 3) != 0);
+            wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
+            wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
+          }
+          const f16x8 va = __builtin_bit_cast(f16x8, wa);
+          const f16x8 vb = __builtin_bit_cast(f16x8, wb);
+#pragma unroll
+          for (int qt = 0; qt < NQT; ++qt) {
+            acc[qt][tp] = mfma16(va, pop[qt], acc[qt][tp]);
+            acc[qt][tp + 1] = mfma16(vb, pop[qt], acc[qt][tp + 1]);
+          }
+        }
+      };
+
+      // ---- main loop: the split's 32-token blocks through kDepth register buffers ----
+      // Block k is computed while blocks k+1 .. k+kDepth-1 are in flight; its
+      // buffer is refilled with block k+kDepth right after.
+      {
+        BlockRaw<D> buf[kDepth];
+#pragma unroll
+        for (int i = 0; i < kDepth; ++i)
+          if (i < nblk) load_block(buf[i], i);
+        for (int k = 0; k < nblk; k += kDepth) {
+#pragma unroll
+          for (int i = 0; i < kDepth; ++i) {
+            if (k + i < nblk) {
+              compute_block(buf[i], k + i);
+              if (k + i + kDepth < nblk) load_block(buf[i], k + i + kDepth);
+            }
+          }
+        }
+      }
+
+      // ---- epilogue: this lane holds column 16*qt + lane%16, dims [DPL*j, DPL*j + DPL) ----
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        const float l_tot = wave_sum_xor16_32(l_run[qt]);
+        const int col = 16 * qt + n16;
+        if (col >= mcols) continue;
+        const float inv = (l_tot > 0.0f) ? v_scale / l_tot : 0.0f;
+        const int g = col / q_len;
+        const int i = col - g * q_len;
+        const int64_t row = (int64_t)b * q_len + i;
+        const int64_t h = (int64_t)kvh * p.group + g;
+        if (direct) {
+          QT *dst = reinterpret_cast<QT *>(p.out) + row * p.o_srow + h * p.o_shead + DPL * j;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            if constexpr (D == 128) {
+              i32x4 w;
+#pragma unroll
+              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<QT>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+              *reinterpret_cast<i32x4 *>(dst + rr * NT) = w;
+            } else {
+              i32x2 w;
+#pragma unroll
+              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<QT>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+              *reinterpret_cast<i32x2 *>(dst + rr * NT) = w;
+            }
+          }
+          if (j == 0 && p.lse) {
+            const float m = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
+            // v_log_f32 is log2
+            p.lse[row * p.lse_srow + h * p.lse_shead] =
+                (l_tot > 0.0f) ? kLn2 * (m + __builtin_amdgcn_logf(l_tot)) : -INFINITY;
+          }
+        } else {
+          const int64_t po_idx = row * p.po_srow + h * p.po_shead + (int64_t)split * p.po_ssplit + DPL * j;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            if (p.po_f32) {
+              float *dst = reinterpret_cast<float *>(p.po) + po_idx + rr * NT;
+#pragma unroll
+              for (int t = 0; t < NT; t += 4)
+                *reinterpret_cast<f32x4 *>(dst + t) = f32x4{acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv,
+                                                            acc[qt][t + 2][rr] * inv, acc[qt][t + 3][rr] * inv};
+            } else {
+              _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx + rr * NT;
+              if constexpr (D == 128) {
+                i32x4 w;
+#pragma unroll
+                for (int t = 0; t < NT; t += 2)
+                  w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+                *reinterpret_cast<i32x4 *>(dst) = w;
+              } else {
+                i32x2 w;
+#pragma unroll
+                for (int t = 0; t < NT; t += 2)
+                  w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+                *reinterpret_cast<i32x2 *>(dst) = w;
+              }
+            }
+          }
+          if (j == 0) {
+            p.pm[row * p.pm_srow + h * p.pm_shead + (int64_t)split * p.pm_ssplit] = m_run[qt];
+            p.pl[row * p.pl_srow + h * p.pl_shead + (int64_t)split * p.pl_ssplit] = l_tot;
+          }
         }
       }
     }
@@ -606,6 +696,34 @@ __global__ void dequant_bf16_kernel(const uint8_t *src, uint16_t *dst, int64_t n
     if (i + e < n) dst[i + e] = (uint16_t)(words[e >> 1] >> (16 * (e & 1)));
 }
 
+// ---------------------------------------------------------------------------
+// HBM calibration kernels: a pure streaming read and a plain copy, used to
+// measure the read ceiling of the device and to scale FETCH_SIZE/WRITE_SIZE.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void stream_read_kernel(const i32x4 *src, int64_t n16, int *sink) {
+  int acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const i32x4 a = __builtin_nontemporal_load(src + i);
+    const i32x4 b = __builtin_nontemporal_load(src + i + stride);
+    const i32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const i32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= a[0] ^ a[1] ^ a[2] ^ a[3] ^ b[0] ^ b[1] ^ b[2] ^ b[3] ^ c[0] ^ c[1] ^ c[2] ^ c[3] ^ d[0] ^ d[1] ^ d[2] ^
+           d[3];
+  }
+  for (; i < n16; i += stride) {
+    const i32x4 a = src[i];
+    acc ^= a[0] ^ a[1] ^ a[2] ^ a[3];
+  }
+  if (acc == 0x7fffffff) sink[blockIdx.x] = acc;  // keeps the loads live; practically never stores
+}
+
+__global__ __launch_bounds__(256) void stream_copy_kernel(const i32x4 *src, i32x4 *dst, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
 }  // namespace l20pd
 
 // ===========================================================================
@@ -651,6 +769,12 @@ int32_t check_args(const l20_pd_fp8_args *a) {
     if (a->partial_dtype != L20_PD_FP32 && a->partial_dtype != L20_PD_FP16)
       return fail(L20_PD_EINVAL, "partial output must be fp32 or fp16");
   }
+  for (int which = 0; which < 2; ++which) {
+    const int64_t st = which ? a->v_stride_token : a->k_stride_token;
+    const int64_t sh = which ? a->v_stride_head : a->k_stride_head;
+    if (st < 0 || sh < 0 || 15 * st + (int64_t)(a->num_kv_heads - 1) * sh + a->head_dim > INT32_MAX)
+      return fail(L20_PD_EINVAL, "K/V token and head strides must be non-negative and span less than 2 GiB per page");
+  }
   if (a->bt_max_pages * (int64_t)16 < a->max_seq_len)
     return fail(L20_PD_EINVAL, "block table has fewer pages than max_seq_len needs");
   // Vector-load alignment: 16 B K chunks, 8/4 B V chunks, 16 B query chunks.
@@ -663,6 +787,12 @@ int32_t check_args(const l20_pd_fp8_args *a) {
     return fail(L20_PD_EINVAL, "V cache pointer and strides must be aligned to head_dim/16 bytes");
   if (((uintptr_t)a->query % 16) != 0 || (a->q_stride_row % 8) != 0 || (a->q_stride_head % 8) != 0)
     return fail(L20_PD_EINVAL, "query pointer and strides must be 16-byte aligned");
+  if (((uintptr_t)a->output % 16) != 0 || (a->o_stride_row % 8) != 0 || (a->o_stride_head % 8) != 0)
+    return fail(L20_PD_EINVAL, "output pointer and strides must be 16-byte aligned");
+  if (n_s > 1 && a->partial_dtype == L20_PD_FP16 &&
+      (((uintptr_t)a->partial_output % 16) != 0 || a->po_stride_row % 8 || a->po_stride_head % 8 ||
+       a->po_stride_split % 8))
+    return fail(L20_PD_EINVAL, "fp16 partial output must be 16-byte aligned");
   if (n_s > 1 && a->partial_dtype == L20_PD_FP32 &&
       (((uintptr_t)a->partial_output % 16) != 0 || a->po_stride_row % 4 || a->po_stride_head % 4 ||
        a->po_stride_split % 4))
@@ -670,11 +800,34 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   return L20_PD_OK;
 }
 
+// Workgroups the persistent partial kernel launches: enough to fill every CU
+// at the kernel's occupancy, never more than there can be work items.
 template <typename QT, int D, int NQT>
-hipError_t launch_partial(const l20pd::PartialParams &pp, int batch, int num_kv_heads, int nwaves,
-                          hipStream_t stream) {
-  dim3 grid(num_kv_heads, batch, pp.num_splits);
-  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), grid, dim3(64 * nwaves), 0, stream, pp);
+int partial_grid(int threads, int64_t max_items) {
+  static thread_local int cached_dev = -1, cached_threads = -1, cached_blocks = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev != cached_dev || threads != cached_threads) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, D, NQT>, threads, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    cached_dev = dev;
+    cached_threads = threads;
+    cached_blocks = cus * per_cu;
+  }
+  return (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, max_items));
+}
+
+template <typename QT, int D, int NQT>
+hipError_t launch_partial(const l20pd::PartialParams &pp, int batch, int num_kv_heads, hipStream_t stream) {
+  const int nwaves = std::min(num_kv_heads, l20pd::kMaxWaves);
+  const int threads = 64 * nwaves;
+  const int64_t max_items = (int64_t)batch * pp.num_splits;
+  const int grid = partial_grid<QT, D, NQT>(threads, max_items);
+  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), dim3(grid), dim3(threads), 0, stream, pp);
   return hipGetLastError();
 }
 
@@ -692,12 +845,15 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.q_shead = a.q_stride_head;
   pp.k = a.key_cache;
   pp.k_spage = a.k_stride_page;
-  pp.k_stok = a.k_stride_token;
-  pp.k_shead = a.k_stride_head;
+  pp.k_stok32 = (int)a.k_stride_token;
+  pp.k_shead32 = (int)a.k_stride_head;
   pp.v = a.value_cache;
   pp.v_spage = a.v_stride_page;
-  pp.v_stok = a.v_stride_token;
-  pp.v_shead = a.v_stride_head;
+  pp.v_stok32 = (int)a.v_stride_token;
+  pp.v_shead32 = (int)a.v_stride_head;
+  // Bytes one KV-head slice of a page can touch: the buffer range of its loads.
+  pp.k_extent = (int)(15 * a.k_stride_token + (int64_t)(a.num_kv_heads - 1) * a.k_stride_head + a.head_dim);
+  pp.v_extent = (int)(15 * a.v_stride_token + (int64_t)(a.num_kv_heads - 1) * a.v_stride_head + a.head_dim);
   pp.bt = a.block_table;
   pp.bt_srow = a.bt_stride_row;
   pp.seq_lens = a.seq_lens;
@@ -735,6 +891,7 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.po_f32 = a.partial_dtype == L20_PD_FP32;
   const int64_t cap = std::min<int64_t>((int64_t)pp.num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
   pp.l_cap = (int)cap;
+  pp.batch = a.batch;
   return pp;
 }
 
@@ -780,8 +937,6 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   const int group = a->num_q_heads / a->num_kv_heads;
   const int nqt = (group * a->q_len + 15) / 16;
-  const int blocks_per_split = (a->split_size + 31) / 32;
-  const int nwaves = blocks_per_split >= 4 ? 4 : blocks_per_split;
   const l20pd::PartialParams pp = partial_params(*a, n_s);
   const l20pd::MergeParams mp = merge_params(*a, pp.num_splits);
   const bool bf16 = a->query_dtype == L20_PD_BF16;
@@ -790,18 +945,18 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages) {
   if (stages & kPartial) {
     if (a->head_dim == 128) {
       if (nqt == 1)
-        e = bf16 ? launch_partial<__bf16, 128, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream)
-                 : launch_partial<_Float16, 128, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+        e = bf16 ? launch_partial<__bf16, 128, 1>(pp, a->batch, a->num_kv_heads, stream)
+                 : launch_partial<_Float16, 128, 1>(pp, a->batch, a->num_kv_heads, stream);
       else
-        e = bf16 ? launch_partial<__bf16, 128, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream)
-                 : launch_partial<_Float16, 128, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+        e = bf16 ? launch_partial<__bf16, 128, 2>(pp, a->batch, a->num_kv_heads, stream)
+                 : launch_partial<_Float16, 128, 2>(pp, a->batch, a->num_kv_heads, stream);
     } else {
       if (nqt == 1)
-        e = bf16 ? launch_partial<__bf16, 64, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream)
-                 : launch_partial<_Float16, 64, 1>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+        e = bf16 ? launch_partial<__bf16, 64, 1>(pp, a->batch, a->num_kv_heads, stream)
+                 : launch_partial<_Float16, 64, 1>(pp, a->batch, a->num_kv_heads, stream);
       else
-        e = bf16 ? launch_partial<__bf16, 64, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream)
-                 : launch_partial<_Float16, 64, 2>(pp, a->batch, a->num_kv_heads, nwaves, stream);
+        e = bf16 ? launch_partial<__bf16, 64, 2>(pp, a->batch, a->num_kv_heads, stream)
+                 : launch_partial<_Float16, 64, 2>(pp, a->batch, a->num_kv_heads, stream);
     }
   }
   // With a single split every row is finished by the partial kernel.
@@ -887,6 +1042,34 @@ int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst, int64_t 
   if (blocks > 0x7fffffff) return fail(L20_PD_EINVAL, "dequant size too large");
   hipLaunchKernelGGL(l20pd::dequant_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), src, dst, n);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
+int32_t l20_pd_stream_read(const void *src, int64_t bytes, int32_t *sink, int32_t blocks, void *stream) {
+  g_last_error[0] = '\0';
+  if (!src || !sink || bytes < 0 || bytes % 16 || ((uintptr_t)src % 16) || blocks <= 0)
+    return fail(L20_PD_EINVAL, "stream_read needs a 16-byte aligned buffer, a multiple of 16 bytes and blocks > 0");
+  hipLaunchKernelGGL(l20pd::stream_read_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const l20pd::i32x4 *>(src), bytes / 16, sink);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
+int32_t l20_pd_stream_copy(const void *src, void *dst, int64_t bytes, int32_t blocks, void *stream) {
+  g_last_error[0] = '\0';
+  if (!src || !dst || bytes < 0 || bytes % 16 || ((uintptr_t)src % 16) || ((uintptr_t)dst % 16) || blocks <= 0)
+    return fail(L20_PD_EINVAL, "stream_copy needs 16-byte aligned buffers, a multiple of 16 bytes and blocks > 0");
+  hipLaunchKernelGGL(l20pd::stream_copy_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const l20pd::i32x4 *>(src), reinterpret_cast<l20pd::i32x4 *>(dst), bytes / 16);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));

@@ -29,6 +29,8 @@ EXPORTED = (
     "l20_pd_default_split_size",
     "l20_pd_fp8_e4m3_dequant_f32",
     "l20_pd_fp8_e4m3_dequant_bf16",
+    "l20_pd_stream_read",
+    "l20_pd_stream_copy",
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -85,6 +87,10 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     lib.l20_pd_fp8_e4m3_dequant_f32.restype = _i32
     lib.l20_pd_fp8_e4m3_dequant_bf16.argtypes = [_vp, _vp, _i64, _vp]
     lib.l20_pd_fp8_e4m3_dequant_bf16.restype = _i32
+    lib.l20_pd_stream_read.argtypes = [_vp, _i64, _vp, _i32, _vp]
+    lib.l20_pd_stream_read.restype = _i32
+    lib.l20_pd_stream_copy.argtypes = [_vp, _vp, _i64, _i32, _vp]
+    lib.l20_pd_stream_copy.restype = _i32
     if path is None:
         _lib = lib
     return lib
