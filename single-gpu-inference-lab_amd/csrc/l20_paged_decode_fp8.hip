@@ -38,6 +38,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <vector>
 
 #include "l20_paged_decode.h"
 
@@ -56,6 +57,7 @@ constexpr int kPage = 16;
 constexpr int kMaxWaves = 8;       // waves per partial workgroup (one per KV head)
 constexpr int kMaxCompactBatch = 8192;  // sequences whose work list fits in LDS
 constexpr int kDepth = 2;               // K/V blocks in flight per wave
+constexpr int kMaxRunTokens = 1024;     // longest run one wave accumulates (64 page ids in a VGPR)
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: dword 3 (format bits)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -174,11 +176,9 @@ template <> __device__ __forceinline__ int pack2<_Float16>(float a, float b) {
   return __builtin_bit_cast(int, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
-// Splits of sequence b: ceil(L / split_size), and one (zero-writing) item
-// for an empty sequence.
-__device__ __forceinline__ int splits_of(const PartialParams &p, int b) {
-  const int L = min(p.seq_lens[b], p.l_cap);
-  return L > 0 ? (L + p.split_size - 1) / p.split_size : 1;
+// Clamped length of sequence b (tokens past l_cap are never touched).
+__device__ __forceinline__ int clamped_len(const PartialParams &p, int b) {
+  return max(0, min(p.seq_lens[b], p.l_cap));
 }
 
 // Inclusive scan of one value per thread over the workgroup (<= 512 threads).
@@ -198,15 +198,112 @@ __device__ __forceinline__ int block_inclusive_scan(int v, int *s_wave) {
   return v + base;
 }
 
-// Persistent, page-major partial kernel.
+__device__ __forceinline__ int lds_uniform(const int *a, int i) { return __builtin_amdgcn_readfirstlane(a[i]); }
+// One run: splits [s_first, s_last] of sequence b (clamped length L, n_b splits).
+struct Run {
+  int b, s_first, s_last, L, n_b;
+};
+
+// Walks the runs of one workgroup's token share.  Tok(i) returns T_i, the
+// token offset of sequence i (T_0 = 0, T_B = total).  Shared by the kernel
+// (Tok reads the LDS prefix) and by l20_pd_plan_runs on the host, so the CPU
+// tests check the exact schedule the GPU runs.  Every call of next() either
+// returns a run of at least one split and moves past it, or ends the walk,
+// so a walk takes at most (number of items) steps.
+template <typename Tok>
+struct RunCursor {
+  Tok tok;
+  int B, S, max_run_items;
+  bool last_share;
+  int64_t share_lo, share_hi;  // [share_lo, share_hi); the last share is unbounded
+  int b, s;
+
+  __host__ __device__ RunCursor(Tok t, int batch, int split, int max_items) : tok(t), B(batch), S(split),
+      max_run_items(max_items), last_share(false), share_lo(0), share_hi(0), b(0), s(0) {}
+
+  __host__ __device__ static int splits_of(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
+
+  // Position on the first item of share w of P: the first item whose start
+  // token tau = T_b + s*S is >= share_lo.
+  __host__ __device__ void init(int64_t w, int64_t P) {
+    const int64_t N = tok(B);
+    share_lo = (w * N + P - 1) / P;
+    last_share = (w + 1 == P);
+    share_hi = last_share ? 0 : ((w + 1) * N + P - 1) / P;
+    int lo = 0, hi = B;  // first b whose last item starts at or after share_lo
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      const int t0 = tok(mid);
+      const int n = splits_of(tok(mid + 1) - t0, S);
+      if ((int64_t)t0 + (int64_t)(n - 1) * S >= share_lo)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    b = lo;
+    s = 0;
+    if (b < B) {
+      const int64_t t0 = tok(b);
+      s = share_lo > t0 ? (int)((share_lo - t0 + S - 1) / S) : 0;
+    }
+  }
+
+  __host__ __device__ bool next(Run &r) {
+    while (b < B) {
+      const int t0 = tok(b);
+      const int L = tok(b + 1) - t0;
+      const int n_b = splits_of(L, S);
+      if (s >= n_b) {
+        ++b;
+        s = 0;
+        continue;
+      }
+      const int64_t tau = (int64_t)t0 + (int64_t)s * S;
+      if (!last_share && tau >= share_hi) return false;
+      // last split of b that starts inside the share
+      int64_t last = last_share ? (int64_t)(n_b - 1) : std::min<int64_t>(n_b - 1, (share_hi - 1 - t0) / S);
+      last = std::min<int64_t>(last, (int64_t)s + max_run_items - 1);
+      last = std::max<int64_t>(last, s);
+      r.b = b;
+      r.s_first = s;
+      r.s_last = (int)last;
+      r.L = L;
+      r.n_b = n_b;
+      s = (int)last + 1;
+      if (s >= n_b) {
+        ++b;
+        s = 0;
+      }
+      return true;
+    }
+    return false;
+  }
+};
+
+struct LdsTok {
+  const int *a;
+  __device__ int operator()(int i) const { return __builtin_amdgcn_readfirstlane(a[i]); }
+};
+
+
+// Persistent, page-major, token-balanced partial kernel.
 //
-// Work items are the (sequence, split) pairs, numbered sequence-major in a
-// compact list built at kernel start from seq_lens (no empty items).  The
-// grid is sized to the machine; workgroup w takes items w, w + grid, ... so
-// consecutive items land on different XCDs and every workgroup gets the same
-// number of items.  Inside a workgroup, wave w owns KV heads w, w + W, ...:
-// the waves of one item read the interleaved per-head pieces of the same
-// 16-token pages at the same time, so the NHD page is fetched as a whole.
+// Items are the (sequence, split) pairs in sequence-major order; item (b, s)
+// starts at token offset tau = T_b + s * split_size in the concatenation of
+// all sequences (T_b = tokens of sequences 0..b-1).  That token space is cut
+// into gridDim.x equal shares and workgroup w takes the items whose tau falls
+// in share w, so every workgroup streams the same amount of K/V whatever the
+// length distribution, and consecutive workgroup ids -- dealt round-robin to
+// the 8 XCDs -- give every XCD the same share.  A workgroup handles its items
+// as runs: maximal groups of consecutive items of one sequence, at most
+// kMaxRunTokens long.  A run that is a whole sequence writes the final output
+// and LSE (and marks split slot 0 with +inf for the merge); any other run
+// writes one partial at its first split slot and marks the slots of its
+// other splits with NaN, which the merge skips.  Inside a workgroup, wave w
+// owns KV heads w, w + W, ...: the waves of one run read the interleaved
+// per-head pieces of the same 16-token pages together, so the NHD page is
+// fetched as a whole.  More than kMaxCompactBatch sequences fall back to one
+// item per run, items striped over the grid.
 template <typename QT, int D, int NQT>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
@@ -215,7 +312,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   constexpr int NT = D / 16;   // 16-row d tiles of the PV product
   constexpr int DPL = D / 4;   // contiguous output dims per lane
 
-  __shared__ int s_prefix[kMaxCompactBatch + 1];
+  __shared__ int s_tok[kMaxCompactBatch + 1];  // s_tok[b] = T_b (saturating)
   __shared__ int s_wave[8];
 
   const int nwaves = blockDim.x >> 6;
@@ -226,45 +323,45 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   const int q_len = p.q_len;
   const int mcols = p.group * q_len;
   const int B = p.batch;
+  const int S = p.split_size;
+  const bool balanced = B <= kMaxCompactBatch;
 
-  // ---- compact work list: s_prefix[b] = first item of sequence b ----
-  const bool compact = B <= kMaxCompactBatch;
-  int total;
-  if (compact) {
+  // ---- token prefix of the clamped lengths ----
+  if (balanced) {
     int carry = 0;
-    if (threadIdx.x == 0) s_prefix[0] = 0;
+    if (threadIdx.x == 0) s_tok[0] = 0;
     for (int base = 0; base < B; base += blockDim.x) {
-      const int b = base + threadIdx.x;
-      const int n = b < B ? splits_of(p, b) : 0;
-      const int incl = block_inclusive_scan(n, s_wave);
-      if (b < B) s_prefix[b + 1] = carry + incl;
+      const int bb = base + threadIdx.x;
+      const int len = bb < B ? clamped_len(p, bb) : 0;
+      const int incl = block_inclusive_scan(len, s_wave);
+      if (bb < B) s_tok[bb + 1] = (int)min<int64_t>((int64_t)carry + incl, INT32_MAX);
       __syncthreads();
-      carry = s_prefix[min(base + (int)blockDim.x, B)];
+      carry = s_tok[min(base + (int)blockDim.x, B)];
     }
-    total = __builtin_amdgcn_readfirstlane(s_prefix[B]);
-  } else {
-    total = B * p.num_splits;
   }
+  RunCursor<LdsTok> cursor(LdsTok{s_tok}, B, S, max(1, kMaxRunTokens / S));
+  if (balanced) cursor.init(blockIdx.x, gridDim.x);
+  int64_t stripe_item = blockIdx.x;  // fallback: striped single items
 
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    int b, split;
-    if (compact) {
-      int lo = 0, hi = B - 1;  // last b with s_prefix[b] <= item
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (__builtin_amdgcn_readfirstlane(s_prefix[mid]) <= item)
-          lo = mid;
-        else
-          hi = mid - 1;
-      }
-      b = lo;
-      split = item - __builtin_amdgcn_readfirstlane(s_prefix[b]);
+  while (true) {
+    Run run;
+    if (balanced) {
+      if (!cursor.next(run)) break;
     } else {
-      b = item / p.num_splits;
-      split = item - b * p.num_splits;
-      if (split >= splits_of(p, b)) continue;  // uniform over the workgroup
+      if (stripe_item >= (int64_t)B * p.num_splits) break;
+      run.b = (int)(stripe_item / p.num_splits);
+      run.s_first = run.s_last = (int)(stripe_item - (int64_t)run.b * p.num_splits);
+      stripe_item += gridDim.x;
+      run.L = clamped_len(p, run.b);
+      run.n_b = RunCursor<LdsTok>::splits_of(run.L, S);
+      if (run.s_first >= run.n_b) continue;  // uniform over the workgroup
     }
-    const int L = min(p.seq_lens[b], p.l_cap);
+    const int rb = run.b;
+    const int L = run.L;
+    const int split = run.s_first;  // partial slot of this run
+    const int s_last = run.s_last;
+    const bool direct = (run.s_first == 0 && run.s_last == run.n_b - 1);
+    const bool has_ws = p.num_splits > 1;
 
     for (int kvh = wave; kvh < p.num_kv_heads; kvh += nwaves) {
       if (L <= 0) {
@@ -274,43 +371,30 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           const int d = idx - col * D;
           const int g = col / q_len;
           const int i = col - g * q_len;
-          const int64_t row = (int64_t)b * q_len + i;
+          const int64_t row = (int64_t)rb * q_len + i;
           const int64_t h = (int64_t)kvh * p.group + g;
           reinterpret_cast<QT *>(p.out)[row * p.o_srow + h * p.o_shead + d] = from_f32<QT>(0.0f);
           if (d == 0 && p.lse) p.lse[row * p.lse_srow + h * p.lse_shead] = -INFINITY;
         }
         continue;
       }
-      const int split_start = split * p.split_size;
-      const int split_end = min(split_start + p.split_size, L);
-      const bool direct = (L + p.split_size - 1) / p.split_size == 1;
-
+      const int b = rb;
+      const int split_start = split * S;                      // run's first token
+      const int split_end = min((s_last + 1) * S, L);          // run's end token
       const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
       const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
       const float c_log2 = k_scale * p.qk_scale_log2;
 
-      // ---- query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16 ----
-      qvec8 qop[NQT][NS];
-      int lim[NQT];  // last visible token for this lane's column
+      // ---- masking limits: last visible token for this lane's column ----
+      int lim[NQT];
 #pragma unroll
       for (int qt = 0; qt < NQT; ++qt) {
         const int col = 16 * qt + n16;
-        const int g = col / q_len;
-        const int i = col - g * q_len;
-        lim[qt] = min(split_end - 1, L - q_len + i);
-        if (col < mcols) {
-          const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
-                           (int64_t)(kvh * p.group + g) * p.q_shead;
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
-            qop[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
-          }
-        } else {
-#pragma unroll
-          for (int s = 0; s < NS; ++s) qop[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
-        }
+        lim[qt] = min(split_end - 1, L - q_len + (col % q_len));
       }
+      // The query operand is loaded after the first K/V loads are issued (the
+      // page-id -> K/V chain is the critical path at the start of a run).
+      qvec8 qop[NQT][NS];
       const int min_lim = min(split_end - 1, L - q_len);
 
       // ---- page ids of the split: lane t -> tile t (a split has <= 64 tiles) ----
@@ -487,6 +571,25 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
 #pragma unroll
         for (int i = 0; i < kDepth; ++i)
           if (i < nblk) load_block(buf[i], i);
+        // ---- query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16 ----
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+          const int col = 16 * qt + n16;
+          const int g = col / q_len;
+          const int i = col - g * q_len;
+          if (col < mcols) {
+            const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
+                             (int64_t)(kvh * p.group + g) * p.q_shead;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+              const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
+              qop[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
+            }
+          } else {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) qop[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
+          }
+        }
         for (int k = 0; k < nblk; k += kDepth) {
 #pragma unroll
           for (int i = 0; i < kDepth; ++i) {
@@ -531,6 +634,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
             p.lse[row * p.lse_srow + h * p.lse_shead] =
                 (l_tot > 0.0f) ? kLn2 * (m + __builtin_amdgcn_logf(l_tot)) : -INFINITY;
           }
+          if (j == 0 && has_ws) p.pm[row * p.pm_srow + h * p.pm_shead] = INFINITY;  // merge: already final
         } else {
           const int64_t po_idx = row * p.po_srow + h * p.po_shead + (int64_t)split * p.po_ssplit + DPL * j;
 #pragma unroll
@@ -559,8 +663,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
             }
           }
           if (j == 0) {
-            p.pm[row * p.pm_srow + h * p.pm_shead + (int64_t)split * p.pm_ssplit] = m_run[qt];
+            float *pm = p.pm + row * p.pm_srow + h * p.pm_shead;
+            pm[(int64_t)split * p.pm_ssplit] = m_run[qt];
             p.pl[row * p.pl_srow + h * p.pl_shead + (int64_t)split * p.pl_ssplit] = l_tot;
+            // The run's later splits hold nothing: NaN tells the merge to skip them.
+            for (int sx = split + 1; sx <= s_last; ++sx) pm[(int64_t)sx * p.pm_ssplit] = __builtin_nanf("");
           }
         }
       }
@@ -585,70 +692,94 @@ struct MergeParams {
   int64_t lse_srow, lse_shead;
   int q_len, split_size, num_splits, po_f32;
   int l_cap;  // same clamp as the partial kernel
+  int rows, num_q_heads;
 };
 
+// One wave per (query row, q head), 4 waves per workgroup.  Lane l owns
+// dims [8c, 8c + 8) of slot group g (c = l % (D/8), g = l / (D/8)), so one
+// step covers 512/D slots with 32-byte loads; the steps' loads are
+// independent, the slot groups are folded with shuffles at the end, and
+// nothing goes through LDS or a barrier.
 template <typename QT, int D>
 __global__ __launch_bounds__(256) void pd_merge(MergeParams p) {
-  constexpr int D4 = D / 4;
-  constexpr int SLOTS = 256 / D4;  // splits processed side by side
-  __shared__ float red[256];
-  __shared__ f32x4 part[SLOTS][D4];
-  __shared__ float wpart[SLOTS];
-
-  const int h = blockIdx.x;
-  const int row = blockIdx.y;
+  constexpr int CH = D / 8;      // 8-dim chunks per row
+  constexpr int SG = 64 / CH;    // slots per step
+  const int lane = threadIdx.x & 63;
+  const int c = lane % CH;
+  const int g = lane / CH;
+  const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= (int64_t)p.rows * p.num_q_heads) return;
+  const int row = (int)(pair / p.num_q_heads);
+  const int h = (int)(pair - (int64_t)row * p.num_q_heads);
   const int b = row / p.q_len;
-  const int L = min(p.seq_lens[b], p.l_cap);
+  const int L = max(0, min(p.seq_lens[b], p.l_cap));
   const int n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
   if (n <= 1) return;  // the partial kernel wrote this row (or the empty row) directly
-  const int tid = threadIdx.x;
-  const int c = tid % D4;
-  const int slot = tid / D4;
-  QT *dst = reinterpret_cast<QT *>(p.out) + (int64_t)row * p.o_srow + (int64_t)h * p.o_shead;
   const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
   const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
-  float mx = -INFINITY;
-  for (int s = tid; s < n; s += 256) mx = fmaxf(mx, pm[(int64_t)s * p.pm_ssplit]);
-  red[tid] = mx;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-    __syncthreads();
-  }
-  const float M = red[0];
-  const float msafe = (M == -INFINITY) ? 0.0f : M;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.0f;
-  const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 4 * c;
-  for (int s = slot; s < n; s += SLOTS) {
-    const float w = __builtin_amdgcn_exp2f(pm[(int64_t)s * p.pm_ssplit] - msafe) * pl[(int64_t)s * p.pl_ssplit];
-    f32x4 o;
-    if (p.po_f32) {
-      o = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p.po) + base + (int64_t)s * p.po_ssplit);
-    } else {
-      const _Float16 *src = reinterpret_cast<const _Float16 *>(p.po) + base + (int64_t)s * p.po_ssplit;
-      o = f32x4{(float)src[0], (float)src[1], (float)src[2], (float)src[3]};
+  // One pass, every load independent: each lane keeps an online merge
+  // (max, weight sum, weighted rows) over the slots of its group; NaN slots
+  // continue a run that started in an earlier slot and are skipped.
+  const bool final_row = pm[0] == INFINITY;  // one run wrote the whole row already
+  float mx = -INFINITY, wsum = 0.0f;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
+#pragma unroll 4
+  for (int s0 = 0; s0 < n; s0 += SG) {
+    const int s = s0 + g;
+    if (s < n) {
+      const float ms = pm[(int64_t)s * p.pm_ssplit];
+      const float ls = pl[(int64_t)s * p.pl_ssplit];
+      const int64_t off = base + (int64_t)s * p.po_ssplit;
+      f32x4 o0, o1;
+      if (p.po_f32) {
+        const float *src = reinterpret_cast<const float *>(p.po) + off;
+        o0 = *reinterpret_cast<const f32x4 *>(src);
+        o1 = *reinterpret_cast<const f32x4 *>(src + 4);
+      } else {
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(p.po) + off);
+        o0 = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+        o1 = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+      }
+      if (ms == ms && ms != -INFINITY) {  // stale continuation slots never enter the sums
+        const float m_new = fmaxf(mx, ms);
+        const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
+        const float w = __builtin_amdgcn_exp2f(ms - m_new) * ls;
+        acc0 = acc0 * a_old + w * o0;
+        acc1 = acc1 * a_old + w * o1;
+        wsum = wsum * a_old + w;
+        mx = m_new;
+      }
     }
-    acc += w * o;
-    wsum += w;
   }
-  part[slot][c] = acc;
-  if (c == 0) wpart[slot] = wsum;
-  __syncthreads();
-  if (slot == 0) {
-    f32x4 o = part[0][c];
-    float W = wpart[0];
-    for (int s = 1; s < SLOTS; ++s) {
-      o += part[s][c];
-      W += wpart[s];
-    }
-    const float inv = (W > 0.0f) ? 1.0f / W : 0.0f;
+  // fold the slot groups (lane bits at and above log2(CH)): LSE-combine
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dst[4 * c + e] = from_f32<QT>(o[e] * inv);
-    if (c == 0 && p.lse) {
-      p.lse[(int64_t)row * p.lse_srow + (int64_t)h * p.lse_shead] =
-          (W > 0.0f) ? kLn2 * (msafe + __builtin_amdgcn_logf(W)) : -INFINITY;
+  for (int off = CH; off < 64; off <<= 1) {
+    const float m_o = __shfl_xor(mx, off);
+    const float m_new = fmaxf(mx, m_o);
+    const float ms = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float a = __builtin_amdgcn_exp2f(mx - ms);
+    const float bo = __builtin_amdgcn_exp2f(m_o - ms);
+    const float w_o = __shfl_xor(wsum, off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc0[e] = acc0[e] * a + __shfl_xor(acc0[e], off) * bo;
+      acc1[e] = acc1[e] * a + __shfl_xor(acc1[e], off) * bo;
     }
+    wsum = wsum * a + w_o * bo;
+    mx = m_new;
+  }
+  const float msafe = (mx == -INFINITY) ? 0.0f : mx;
+  if (final_row) return;
+  if (g != 0) return;
+  const float inv = (wsum > 0.0f) ? 1.0f / wsum : 0.0f;
+  QT *dst = reinterpret_cast<QT *>(p.out) + (int64_t)row * p.o_srow + (int64_t)h * p.o_shead + 8 * c;
+  const i32x4 w = {pack2<QT>(acc0[0] * inv, acc0[1] * inv), pack2<QT>(acc0[2] * inv, acc0[3] * inv),
+                   pack2<QT>(acc1[0] * inv, acc1[1] * inv), pack2<QT>(acc1[2] * inv, acc1[3] * inv)};
+  *reinterpret_cast<i32x4 *>(dst) = w;
+  if (c == 0 && p.lse) {
+    p.lse[(int64_t)row * p.lse_srow + (int64_t)h * p.lse_shead] =
+        (wsum > 0.0f) ? kLn2 * (msafe + __builtin_amdgcn_logf(wsum)) : -INFINITY;
   }
 }
 
@@ -833,7 +964,8 @@ hipError_t launch_partial(const l20pd::PartialParams &pp, int batch, int num_kv_
 
 template <typename QT, int D>
 hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipStream_t stream) {
-  hipLaunchKernelGGL((l20pd::pd_merge<QT, D>), dim3(heads, rows), dim3(256), 0, stream, mp);
+  const int64_t pairs = (int64_t)rows * heads;
+  hipLaunchKernelGGL((l20pd::pd_merge<QT, D>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, stream, mp);
   return hipGetLastError();
 }
 
@@ -922,6 +1054,8 @@ l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
   mp.num_splits = num_splits;
   mp.po_f32 = a.partial_dtype == L20_PD_FP32;
   mp.l_cap = (int)std::min<int64_t>((int64_t)num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
+  mp.rows = a.batch * a.q_len;
+  mp.num_q_heads = a.num_q_heads;
   return mp;
 }
 
@@ -1048,6 +1182,39 @@ int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst, int64_t 
     return L20_PD_ELAUNCH;
   }
   return L20_PD_OK;
+}
+
+int32_t l20_pd_plan_runs(const int32_t *seq_lens, int32_t batch, int32_t split_size, int32_t l_cap, int32_t grid,
+                         int32_t *runs, int32_t max_runs) {
+  g_last_error[0] = '\0';
+  if (!seq_lens || batch < 0 || split_size <= 0 || grid <= 0 || max_runs < 0 || (max_runs > 0 && !runs))
+    return fail(-1, "invalid plan arguments");
+  struct HostTok {
+    const int *a;
+    int operator()(int i) const { return a[i]; }
+  };
+  std::vector<int> tok((size_t)batch + 1, 0);
+  for (int b = 0; b < batch; ++b) {
+    const int len = std::max(0, std::min(seq_lens[b], l_cap));
+    tok[b + 1] = (int)std::min<int64_t>((int64_t)tok[b] + len, INT32_MAX);
+  }
+  int32_t count = 0;
+  for (int w = 0; w < grid; ++w) {
+    l20pd::RunCursor<HostTok> cursor(HostTok{tok.data()}, batch, split_size,
+                                     std::max(1, l20pd::kMaxRunTokens / split_size));
+    cursor.init(w, grid);
+    l20pd::Run r;
+    while (cursor.next(r)) {
+      if (count < max_runs) {
+        runs[4 * count + 0] = w;
+        runs[4 * count + 1] = r.b;
+        runs[4 * count + 2] = r.s_first;
+        runs[4 * count + 3] = r.s_last;
+      }
+      ++count;
+    }
+  }
+  return count;
 }
 
 int32_t l20_pd_stream_read(const void *src, int64_t bytes, int32_t *sink, int32_t blocks, void *stream) {
