@@ -151,19 +151,6 @@ int32_t l20_pd_fp8_e4m3_dequant_f32(const uint8_t *src, float *dst, int64_t n,
 int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst,
                                      int64_t n, void *stream);
 
-/* Host mirror of the partial kernel's schedule (no reference counterpart;
- * the reference launches one CTA per (q head, split, sequence)).  The
- * kernel cuts the concatenated token space of the clamped sequence lengths
- * (min(seq_lens[b], l_cap), l_cap = min(num_splits * split_size, 16 *
- * bt_max_pages)) into `grid` equal shares and each workgroup walks the
- * (sequence, split) items starting in its share as runs of consecutive
- * splits of one sequence.  Writes up to max_runs runs as int32 quadruples
- * (workgroup, sequence, first split, last split) and returns the total
- * number of runs (-1 on invalid arguments).  CPU only. */
-int32_t l20_pd_plan_runs(const int32_t *seq_lens, int32_t batch,
-                         int32_t split_size, int32_t l_cap, int32_t grid,
-                         int32_t *runs, int32_t max_runs);
-
 /* HBM calibration (no reference counterpart; measurement support).
  * stream_read reads `bytes` once with 16-byte nontemporal loads over
  * `blocks` workgroups of 256 threads (sink: int32 [blocks], practically never

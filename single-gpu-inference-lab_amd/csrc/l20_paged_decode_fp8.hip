@@ -38,7 +38,6 @@
 #include <string.h>
 
 #include <algorithm>
-#include <vector>
 
 #include "l20_paged_decode.h"
 
@@ -55,7 +54,7 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPage = 16;
 constexpr int kMaxWaves = 8;       // waves per partial workgroup (one per KV head)
-constexpr int kMaxCompactBatch = 8192;  // sequences whose work list fits in LDS
+constexpr int kMaxCompactBatch = 4096;  // sequences whose work list fits in LDS
 constexpr int kDepth = 2;               // K/V blocks in flight per wave
 constexpr int kMaxRunTokens = 1024;     // longest run one wave accumulates (64 page ids in a VGPR)
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: dword 3 (format bits)
@@ -199,111 +198,28 @@ __device__ __forceinline__ int block_inclusive_scan(int v, int *s_wave) {
 }
 
 __device__ __forceinline__ int lds_uniform(const int *a, int i) { return __builtin_amdgcn_readfirstlane(a[i]); }
-// One run: splits [s_first, s_last] of sequence b (clamped length L, n_b splits).
-struct Run {
-  int b, s_first, s_last, L, n_b;
-};
 
-// Walks the runs of one workgroup's token share.  Tok(i) returns T_i, the
-// token offset of sequence i (T_0 = 0, T_B = total).  Shared by the kernel
-// (Tok reads the LDS prefix) and by l20_pd_plan_runs on the host, so the CPU
-// tests check the exact schedule the GPU runs.  Every call of next() either
-// returns a run of at least one split and moves past it, or ends the walk,
-// so a walk takes at most (number of items) steps.
-template <typename Tok>
-struct RunCursor {
-  Tok tok;
-  int B, S, max_run_items;
-  bool last_share;
-  int64_t share_lo, share_hi;  // [share_lo, share_hi); the last share is unbounded
-  int b, s;
+__device__ __forceinline__ int splits_of_len(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
+// Work queue of the persistent partial kernel: [0] next item, [1] workgroups
+// finished.  Zero at load; the last workgroup to finish a launch resets both,
+// so every launch starts from zero without a memset (and a captured graph
+// replays correctly).  Launches on one device must therefore not overlap.
+__device__ unsigned int g_pd_queue[2];
 
-  __host__ __device__ RunCursor(Tok t, int batch, int split, int max_items) : tok(t), B(batch), S(split),
-      max_run_items(max_items), last_share(false), share_lo(0), share_hi(0), b(0), s(0) {}
-
-  __host__ __device__ static int splits_of(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
-
-  // Position on the first item of share w of P: the first item whose start
-  // token tau = T_b + s*S is >= share_lo.
-  __host__ __device__ void init(int64_t w, int64_t P) {
-    const int64_t N = tok(B);
-    share_lo = (w * N + P - 1) / P;
-    last_share = (w + 1 == P);
-    share_hi = last_share ? 0 : ((w + 1) * N + P - 1) / P;
-    int lo = 0, hi = B;  // first b whose last item starts at or after share_lo
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      const int t0 = tok(mid);
-      const int n = splits_of(tok(mid + 1) - t0, S);
-      if ((int64_t)t0 + (int64_t)(n - 1) * S >= share_lo)
-        hi = mid;
-      else
-        lo = mid + 1;
-    }
-    b = lo;
-    s = 0;
-    if (b < B) {
-      const int64_t t0 = tok(b);
-      s = share_lo > t0 ? (int)((share_lo - t0 + S - 1) / S) : 0;
-    }
-  }
-
-  __host__ __device__ bool next(Run &r) {
-    while (b < B) {
-      const int t0 = tok(b);
-      const int L = tok(b + 1) - t0;
-      const int n_b = splits_of(L, S);
-      if (s >= n_b) {
-        ++b;
-        s = 0;
-        continue;
-      }
-      const int64_t tau = (int64_t)t0 + (int64_t)s * S;
-      if (!last_share && tau >= share_hi) return false;
-      // last split of b that starts inside the share
-      int64_t last = last_share ? (int64_t)(n_b - 1) : std::min<int64_t>(n_b - 1, (share_hi - 1 - t0) / S);
-      last = std::min<int64_t>(last, (int64_t)s + max_run_items - 1);
-      last = std::max<int64_t>(last, s);
-      r.b = b;
-      r.s_first = s;
-      r.s_last = (int)last;
-      r.L = L;
-      r.n_b = n_b;
-      s = (int)last + 1;
-      if (s >= n_b) {
-        ++b;
-        s = 0;
-      }
-      return true;
-    }
-    return false;
-  }
-};
-
-struct LdsTok {
-  const int *a;
-  __device__ int operator()(int i) const { return __builtin_amdgcn_readfirstlane(a[i]); }
-};
-
-
-// Persistent, page-major, token-balanced partial kernel.
+// Persistent, page-major partial kernel with a dynamic work queue.
 //
-// Items are the (sequence, split) pairs in sequence-major order; item (b, s)
-// starts at token offset tau = T_b + s * split_size in the concatenation of
-// all sequences (T_b = tokens of sequences 0..b-1).  That token space is cut
-// into gridDim.x equal shares and workgroup w takes the items whose tau falls
-// in share w, so every workgroup streams the same amount of K/V whatever the
-// length distribution, and consecutive workgroup ids -- dealt round-robin to
-// the 8 XCDs -- give every XCD the same share.  A workgroup handles its items
-// as runs: maximal groups of consecutive items of one sequence, at most
-// kMaxRunTokens long.  A run that is a whole sequence writes the final output
-// and LSE (and marks split slot 0 with +inf for the merge); any other run
-// writes one partial at its first split slot and marks the slots of its
-// other splits with NaN, which the merge skips.  Inside a workgroup, wave w
-// owns KV heads w, w + W, ...: the waves of one run read the interleaved
+// Items are the (sequence, split) pairs in sequence-major order, numbered
+// through a prefix of the per-sequence split counts that every workgroup
+// builds in LDS at start (no empty items).  Workgroups claim items one at a
+// time from g_pd_queue, so faster CUs simply take more items and the launch
+// ends within about one item of perfect balance.  Inside a workgroup, wave w
+// owns KV heads w, w + W, ...: the waves of one item read the interleaved
 // per-head pieces of the same 16-token pages together, so the NHD page is
-// fetched as a whole.  More than kMaxCompactBatch sequences fall back to one
-// item per run, items striped over the grid.
+// fetched as a whole.  An item of a single-split sequence writes the final
+// output and LSE (and marks split slot 0 with +inf for the merge); any other
+// item writes its fp32 partial (o / l, m, l) at its split slot.  More than
+// kMaxCompactBatch sequences fall back to numbering items sequence-major over
+// all num_splits slots and skipping the empty ones.
 template <typename QT, int D, int NQT>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
@@ -312,8 +228,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   constexpr int NT = D / 16;   // 16-row d tiles of the PV product
   constexpr int DPL = D / 4;   // contiguous output dims per lane
 
-  __shared__ int s_tok[kMaxCompactBatch + 1];  // s_tok[b] = T_b (saturating)
+  __shared__ int s_prefix[kMaxCompactBatch + 1];  // s_prefix[b] = first item of sequence b
+  __shared__ int s_len[kMaxCompactBatch];         // clamped length of sequence b
   __shared__ int s_wave[8];
+  __shared__ int s_item;
 
   const int nwaves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -324,43 +242,59 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   const int mcols = p.group * q_len;
   const int B = p.batch;
   const int S = p.split_size;
-  const bool balanced = B <= kMaxCompactBatch;
+  const bool compact = B <= kMaxCompactBatch;
 
-  // ---- token prefix of the clamped lengths ----
-  if (balanced) {
+  // ---- item numbering: prefix of the split counts ----
+  int total;
+  if (compact) {
     int carry = 0;
-    if (threadIdx.x == 0) s_tok[0] = 0;
+    if (threadIdx.x == 0) s_prefix[0] = 0;
     for (int base = 0; base < B; base += blockDim.x) {
       const int bb = base + threadIdx.x;
       const int len = bb < B ? clamped_len(p, bb) : 0;
-      const int incl = block_inclusive_scan(len, s_wave);
-      if (bb < B) s_tok[bb + 1] = (int)min<int64_t>((int64_t)carry + incl, INT32_MAX);
+      const int n = bb < B ? splits_of_len(len, S) : 0;
+      const int incl = block_inclusive_scan(n, s_wave);
+      if (bb < B) {
+        s_prefix[bb + 1] = carry + incl;
+        s_len[bb] = len;
+      }
       __syncthreads();
-      carry = s_tok[min(base + (int)blockDim.x, B)];
+      carry = s_prefix[min(base + (int)blockDim.x, B)];
     }
+    total = lds_uniform(s_prefix, B);
+  } else {
+    total = B * p.num_splits;
   }
-  RunCursor<LdsTok> cursor(LdsTok{s_tok}, B, S, max(1, kMaxRunTokens / S));
-  if (balanced) cursor.init(blockIdx.x, gridDim.x);
-  int64_t stripe_item = blockIdx.x;  // fallback: striped single items
 
-  while (true) {
-    Run run;
-    if (balanced) {
-      if (!cursor.next(run)) break;
+  // The first item of workgroup w is item w; later items are claimed from the
+  // queue, one claim ahead: the claim for the next item is issued when the
+  // current one starts and only read when it ends, so its latency overlaps
+  // the work and the claims of different workgroups spread out in time.
+  int item = blockIdx.x;
+  while (item < total) {
+    unsigned int next_claim = 0;
+    if (threadIdx.x == 0) next_claim = gridDim.x + atomicAdd(&g_pd_queue[0], 1u);
+    int rb, split;
+    if (compact) {
+      int lo = 0, hi = B - 1;  // last b with s_prefix[b] <= item
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (lds_uniform(s_prefix, mid) <= item)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      rb = lo;
+      split = item - lds_uniform(s_prefix, rb);
     } else {
-      if (stripe_item >= (int64_t)B * p.num_splits) break;
-      run.b = (int)(stripe_item / p.num_splits);
-      run.s_first = run.s_last = (int)(stripe_item - (int64_t)run.b * p.num_splits);
-      stripe_item += gridDim.x;
-      run.L = clamped_len(p, run.b);
-      run.n_b = RunCursor<LdsTok>::splits_of(run.L, S);
-      if (run.s_first >= run.n_b) continue;  // uniform over the workgroup
+      rb = item / p.num_splits;
+      split = item - rb * p.num_splits;
     }
-    const int rb = run.b;
-    const int L = run.L;
-    const int split = run.s_first;  // partial slot of this run
-    const int s_last = run.s_last;
-    const bool direct = (run.s_first == 0 && run.s_last == run.n_b - 1);
+    const int L = compact ? lds_uniform(s_len, rb) : clamped_len(p, rb);
+    const int n_b = splits_of_len(L, S);
+    if (split < n_b) {  // false only for the fallback numbering; uniform over the workgroup
+    const int s_last = split;
+    const bool direct = n_b == 1;
     const bool has_ws = p.num_splits > 1;
 
     for (int kvh = wave; kvh < p.num_kv_heads; kvh += nwaves) {
@@ -666,11 +600,24 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
             float *pm = p.pm + row * p.pm_srow + h * p.pm_shead;
             pm[(int64_t)split * p.pm_ssplit] = m_run[qt];
             p.pl[row * p.pl_srow + h * p.pl_shead + (int64_t)split * p.pl_ssplit] = l_tot;
-            // The run's later splits hold nothing: NaN tells the merge to skip them.
-            for (int sx = split + 1; sx <= s_last; ++sx) pm[(int64_t)sx * p.pm_ssplit] = __builtin_nanf("");
           }
         }
       }
+    }
+    }  // split < n_b
+    if (threadIdx.x == 0) s_item = (int)next_claim;
+    __syncthreads();
+    item = __builtin_amdgcn_readfirstlane(s_item);
+    __syncthreads();  // s_item is rewritten by the next claim
+  }
+  // ---- end of the launch: the last workgroup out resets the queue ----
+  // No fence: the counters order nothing else, and the kernel boundary
+  // publishes the reset (a fence here would write back the XCD's L2).
+  if (threadIdx.x == 0) {
+    const unsigned int done = atomicAdd(&g_pd_queue[1], 1u);
+    if (done == gridDim.x - 1) {
+      g_pd_queue[0] = 0u;
+      g_pd_queue[1] = 0u;
     }
   }
 }
@@ -1182,39 +1129,6 @@ int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst, int64_t 
     return L20_PD_ELAUNCH;
   }
   return L20_PD_OK;
-}
-
-int32_t l20_pd_plan_runs(const int32_t *seq_lens, int32_t batch, int32_t split_size, int32_t l_cap, int32_t grid,
-                         int32_t *runs, int32_t max_runs) {
-  g_last_error[0] = '\0';
-  if (!seq_lens || batch < 0 || split_size <= 0 || grid <= 0 || max_runs < 0 || (max_runs > 0 && !runs))
-    return fail(-1, "invalid plan arguments");
-  struct HostTok {
-    const int *a;
-    int operator()(int i) const { return a[i]; }
-  };
-  std::vector<int> tok((size_t)batch + 1, 0);
-  for (int b = 0; b < batch; ++b) {
-    const int len = std::max(0, std::min(seq_lens[b], l_cap));
-    tok[b + 1] = (int)std::min<int64_t>((int64_t)tok[b] + len, INT32_MAX);
-  }
-  int32_t count = 0;
-  for (int w = 0; w < grid; ++w) {
-    l20pd::RunCursor<HostTok> cursor(HostTok{tok.data()}, batch, split_size,
-                                     std::max(1, l20pd::kMaxRunTokens / split_size));
-    cursor.init(w, grid);
-    l20pd::Run r;
-    while (cursor.next(r)) {
-      if (count < max_runs) {
-        runs[4 * count + 0] = w;
-        runs[4 * count + 1] = r.b;
-        runs[4 * count + 2] = r.s_first;
-        runs[4 * count + 3] = r.s_last;
-      }
-      ++count;
-    }
-  }
-  return count;
 }
 
 int32_t l20_pd_stream_read(const void *src, int64_t bytes, int32_t *sink, int32_t blocks, void *stream) {

@@ -29,7 +29,6 @@ EXPORTED = (
     "l20_pd_default_split_size",
     "l20_pd_fp8_e4m3_dequant_f32",
     "l20_pd_fp8_e4m3_dequant_bf16",
-    "l20_pd_plan_runs",
     "l20_pd_stream_read",
     "l20_pd_stream_copy",
 )
@@ -88,8 +87,6 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     lib.l20_pd_fp8_e4m3_dequant_f32.restype = _i32
     lib.l20_pd_fp8_e4m3_dequant_bf16.argtypes = [_vp, _vp, _i64, _vp]
     lib.l20_pd_fp8_e4m3_dequant_bf16.restype = _i32
-    lib.l20_pd_plan_runs.argtypes = [_vp, _i32, _i32, _i32, _i32, _vp, _i32]
-    lib.l20_pd_plan_runs.restype = _i32
     lib.l20_pd_stream_read.argtypes = [_vp, _i64, _vp, _i32, _vp]
     lib.l20_pd_stream_read.restype = _i32
     lib.l20_pd_stream_copy.argtypes = [_vp, _vp, _i64, _i32, _vp]
@@ -173,20 +170,6 @@ def partial(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = No
 def merge(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
     """Enqueue only the LSE merge kernel."""
     _call("l20_pd_fp8_e4m3_merge", args, stream, lib)
-
-
-def plan_runs(seq_lens, split_size: int, l_cap: int, grid: int, lib: Optional[ctypes.CDLL] = None):
-    """The partial kernel's schedule as a list of (workgroup, sequence, first split, last split)."""
-    import numpy as np
-
-    lib = lib or load()
-    lens = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.int32))
-    n = lib.l20_pd_plan_runs(lens.ctypes.data, len(lens), split_size, l_cap, grid, None, 0)
-    if n < 0:
-        raise RuntimeError(last_error(lib))
-    out = np.zeros((max(n, 1), 4), dtype=np.int32)
-    lib.l20_pd_plan_runs(lens.ctypes.data, len(lens), split_size, l_cap, grid, out.ctypes.data, n)
-    return [tuple(int(v) for v in row) for row in out[:n]]
 
 
 def check(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> None:
