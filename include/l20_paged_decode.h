@@ -137,8 +137,9 @@ int32_t l20_pd_fp8_e4m3_partial(const l20_pd_fp8_args *args, void *stream);
 int32_t l20_pd_fp8_e4m3_merge(const l20_pd_fp8_args *args, void *stream);
 
 /* Split size the library picks for a call shape when the caller has no
- * preference: a multiple of 16 in [64, 1024] that gives enough
- * (sequence, kv head, split) work items for `cu_count` compute units. */
+ * preference: a power of two in [64, 1024] -- 1024 above 32768 tokens, else
+ * 512, halved while a max_seq_len sequence would have fewer than ~8 splits.
+ * (The reference hook passes a fixed 512, install_l20_fp8_paged_decode.py.) */
 int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads,
                                   int32_t max_seq_len, int32_t cu_count);
 

@@ -2,11 +2,14 @@
 //
 // Two kernels per call, both enqueued on the caller's stream:
 //
-//  pd_fp8_partial<QT, D, NQT>   grid (num_kv_heads, batch, num_splits), 1-4 waves.
-//    One workgroup owns one (sequence, KV head, split) work item and computes
-//    attention for ALL query rows of that KV head (GQA group x q_len, padded to
-//    16 * NQT MFMA columns), so each K/V page is read from HBM exactly once.
-//    The split's 16-token pages are dealt to the waves in 32-token blocks.
+//  pd_fp8_partial<QT, D, NQT>   persistent: CUs x occupancy workgroups, one
+//    wave per KV head (W waves, W the largest divisor of Hkv up to 8).
+//    A work item is one (sequence, split) pair; every wave of the workgroup
+//    computes attention for ALL query rows of its KV head (GQA group x
+//    q_len, padded to 16 * NQT MFMA columns), so each K/V page is read from
+//    HBM exactly once.  Each wave streams 32-token blocks through two
+//    register buffers without draining between items (the next item's page
+//    ids, query and first blocks load while the current one finishes).
 //    Per block and lane:
 //      K: 2 tiles x D/64 x 16 B loads (token = lane%16, 64-byte half-rows),
 //         fp8 -> bf16/f16 conversion (exact), S^T = K . Q^T on
@@ -17,11 +20,10 @@
 //      V: 8 tokens x D/16 contiguous bytes per lane; the fp8 -> f32 -> f16
 //         conversion packs token pairs, which transposes V for the MFMA A
 //         operand in registers (no LDS pass).  O^T += V^T . P^T with P in f16.
-//    The waves' (m, l, O) are combined through LDS.  A sequence with a single
-//    split writes the final output and LSE; otherwise the fp32 partial
-//    (O / l, m, l) goes to the caller's workspace.
+//    A sequence with a single split writes the final output and LSE;
+//    otherwise the fp32 partial (O / l, m, l) goes to the caller's workspace.
 //
-//  pd_merge<QT, D>   grid (num_q_heads, batch*q_len), 256 threads.
+//  pd_merge<QT, D>   one wave per (query row, q head), 4 per workgroup.
 //    LSE merge of a row's splits: M = max m_s, w_s = 2^(m_s - M) l_s,
 //    out = sum w_s o_s / sum w_s, lse = ln2 (M + log2 sum w_s).
 //
@@ -35,6 +37,7 @@
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -55,8 +58,9 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr int kPage = 16;
 constexpr int kMaxWaves = 8;       // waves per partial workgroup (one per KV head)
 constexpr int kMaxCompactBatch = 4096;  // sequences whose work list fits in LDS
-constexpr int kDepth = 2;               // K/V blocks in flight per wave
-constexpr int kMaxRunTokens = 1024;     // longest run one wave accumulates (64 page ids in a VGPR)
+constexpr int kClaimLead = 9;    // blocks before a unit's end at which its successor is claimed
+constexpr int kPublishLead = 6;  // ... published by wave 0 and first polled by the other waves
+constexpr int kNeedLead = 3;     // ... at the latest picked up (its first block loads two blocks later)
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: dword 3 (format bits)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -93,6 +97,8 @@ struct PartialParams {
   int po_f32;
   int l_cap;  // min(num_splits * split_size, block-table pages * 16): tokens past it are never touched
   int batch;
+  int bt_pages;  // block-table row length
+  int compact;   // queue items numbered through an LDS prefix (batch <= 8 * threads)
 };
 
 // ---------------------------------------------------------------------------
@@ -200,26 +206,50 @@ __device__ __forceinline__ int block_inclusive_scan(int v, int *s_wave) {
 __device__ __forceinline__ int lds_uniform(const int *a, int i) { return __builtin_amdgcn_readfirstlane(a[i]); }
 
 __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
-// Work queue of the persistent partial kernel: [0] next item, [1] workgroups
-// finished.  Zero at load; the last workgroup to finish a launch resets both,
-// so every launch starts from zero without a memset (and a captured graph
-// replays correctly).  Launches on one device must therefore not overlap.
+// Work queue of the persistent partial kernel: [0] next queue item, [1]
+// workgroups finished.  Zero at load; the last workgroup to finish a launch
+// resets both, so every launch starts from zero without a memset (and a
+// captured graph replays correctly).  Launches on one device must therefore
+// not overlap.
 __device__ unsigned int g_pd_queue[2];
 
-// Persistent, page-major partial kernel with a dynamic work queue.
+// Splits of sequence b taken by the static first round: workgroup w starts
+// on slot w of the split-major numbering (sequence w % B, split w / B).
+__device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G ? (G - 1 - b) / B + 1 : 0; }
+
+// Persistent, page-major partial kernel: a continuous K/V block stream per wave.
 //
-// Items are the (sequence, split) pairs in sequence-major order, numbered
-// through a prefix of the per-sequence split counts that every workgroup
-// builds in LDS at start (no empty items).  Workgroups claim items one at a
-// time from g_pd_queue, so faster CUs simply take more items and the launch
-// ends within about one item of perfect balance.  Inside a workgroup, wave w
-// owns KV heads w, w + W, ...: the waves of one item read the interleaved
-// per-head pieces of the same 16-token pages together, so the NHD page is
-// fetched as a whole.  An item of a single-split sequence writes the final
-// output and LSE (and marks split slot 0 with +inf for the merge); any other
-// item writes its fp32 partial (o / l, m, l) at its split slot.  More than
-// kMaxCompactBatch sequences fall back to numbering items sequence-major over
-// all num_splits slots and skipping the empty ones.
+// Work items are (sequence, split) pairs; a unit is one KV head of an item.
+// Wave w of a workgroup owns KV heads w, w + W, ... of every item the
+// workgroup takes, so the waves of an item read the interleaved per-head
+// pieces of the same 16-token pages together and the NHD page is fetched as
+// a whole.
+//
+// Item order.  Workgroup w first takes slot w of the split-major numbering
+// (sequence w % B, split w / B), which needs no prefix: its page ids and the
+// sequence length are fetched together, so the first K/V loads leave after
+// one round trip.  The remaining items form the queue: with at most
+// kMaxCompactBatch sequences (compact mode) queue index c is decoded through
+// an LDS prefix of the per-sequence counts of items left after the static
+// round (no empty items); otherwise c continues the split-major numbering and
+// the claiming wave skips its holes.  Workgroups claim queue items one at a
+// time from one counter, in order.  An item's successor is
+// claimed only a few blocks before the item ends (a workgroup never holds an
+// unstarted item for long, so the queue stays balanced to the end) and is
+// published to all waves early enough for the tail of the item to stream its
+// first blocks.
+//
+// Block stream.  A wave keeps two 32-token blocks of raw fp8 K/V in
+// registers.  After computing block k of unit U it refills that buffer with
+// stream position k + 2: U's own block, or one of the first two blocks of
+// the next unit N, whose page ids (and, for one query tile, query operand)
+// are loaded a few blocks before U ends.  The stream never drains between units; block
+// k of a unit sits in buffer (k + par) & 1, par carried over from unit to
+// unit.
+//
+// An item of a single-split sequence writes the final output and LSE (and
+// marks split slot 0 with +inf for the merge); any other item writes its
+// fp32 partial (o / l, m, l) at its split slot.
 template <typename QT, int D, int NQT>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
@@ -227,11 +257,16 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
   constexpr int NT = D / 16;   // 16-row d tiles of the PV product
   constexpr int DPL = D / 4;   // contiguous output dims per lane
+  // One query tile: the next unit's query operand is prefetched into a second
+  // register set.  Two tiles: it is loaded once the current unit's last block
+  // has been computed.
+  constexpr bool kQPrefetch = NQT == 1;
 
-  __shared__ int s_prefix[kMaxCompactBatch + 1];  // s_prefix[b] = first item of sequence b
-  __shared__ int s_len[kMaxCompactBatch];         // clamped length of sequence b
-  __shared__ int s_wave[8];
-  __shared__ int s_item;
+  extern __shared__ int s_dyn[];  // compact mode: s_prefix[B + 1], s_len[B]
+  __shared__ volatile int s_pub[2][3];  // published item (b, s, L); b = -1: none
+  __shared__ volatile int s_seq[2];     // item number of the slot's contents
+  __shared__ int s_ack[2];              // waves other than 0 that have read the slot
+  __shared__ volatile int s_prefix_ready;
 
   const int nwaves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -242,108 +277,354 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   const int mcols = p.group * q_len;
   const int B = p.batch;
   const int S = p.split_size;
-  const bool compact = B <= kMaxCompactBatch;
+  const int G = gridDim.x;
+  const int hpw = p.num_kv_heads / nwaves;  // units per item and wave
+  const bool compact = p.compact != 0;
+  int *s_prefix = s_dyn;      // s_prefix[b]: queue items of sequences < b
+  int *s_len = s_dyn + B + 1;  // clamped length of sequence b
 
-  // ---- item numbering: prefix of the split counts ----
-  int total;
-  if (compact) {
-    int carry = 0;
-    if (threadIdx.x == 0) s_prefix[0] = 0;
-    for (int base = 0; base < B; base += blockDim.x) {
-      const int bb = base + threadIdx.x;
-      const int len = bb < B ? clamped_len(p, bb) : 0;
-      const int n = bb < B ? splits_of_len(len, S) : 0;
-      const int incl = block_inclusive_scan(n, s_wave);
-      if (bb < B) {
-        s_prefix[bb + 1] = carry + incl;
-        s_len[bb] = len;
-      }
-      __syncthreads();
-      carry = s_prefix[min(base + (int)blockDim.x, B)];
+  // ---- per-wave helpers ----
+  auto n_blocks = [&](int s, int L) {
+    const int start = s * S;
+    const int tiles = max(0, (min(start + S, L) - start + kPage - 1) / kPage);
+    return (tiles + 1) >> 1;
+  };
+  // Page ids of split s of sequence b: lane t -> tile t (a split has <= 64
+  // tiles); -1 for tiles past the split and for out-of-range ids.
+  auto load_pid = [&](int b, int s, int L) {
+    const int start = s * S;
+    const int tiles = max(0, (min(start + S, L) - start + kPage - 1) / kPage);
+    int v = -1;
+    if (lane < tiles) {
+      v = p.bt[(int64_t)b * p.bt_srow + start / kPage + lane];
+      v = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
     }
-    total = lds_uniform(s_prefix, B);
-  } else {
-    total = B * p.num_splits;
+    return v;
+  };
+  // Query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16.
+  auto load_q = [&](int b, int kvh, qvec8 (&dst)[NQT][NS]) {
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const int col = 16 * qt + n16;
+      const int g = col / q_len;
+      const int i = col - g * q_len;
+      if (col < mcols) {
+        const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
+                         (int64_t)(kvh * p.group + g) * p.q_shead;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
+          dst[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dst[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
+      }
+    }
+  };
+  // Raw buffer loads through a per-page resource: the page base lives in
+  // SGPRs, one 32-bit lane offset serves every K (V) load of the page and the
+  // hardware range check (the page's byte extent) returns zeros for anything
+  // outside it.  Loads are unconditional -- an invalid page id reads page 0 --
+  // and compute_block zeroes V of every token outside the split or on an
+  // invalid page.  Lane offsets inside a page fit in 32 bits (checked on the
+  // host).
+  auto load_block = [&](BlockRaw<D> &r, int pid, int kvh, int blk) {
+    const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
+    const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
+      const int page = raw_page >= 0 ? raw_page : 0;
+      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, 0));
+      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (D == 128)
+          r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, 0));
+        else
+          r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, 0);
+      }
+    }
+  };
+
+  // ---- stream state (wave-uniform except the VGPR operands) ----
+  BlockRaw<D> buf[2];
+  qvec8 qop[NQT][NS];
+  qvec8 qopN[kQPrefetch ? NQT : 1][NS];
+  int pidU = -1;
+  int par = 0;         // block k of the current unit is in buf[(k + par) & 1]
+  int issuedU = 0;     // blocks of the current unit already loading
+  bool u_loaded = false;  // page ids and query of the current unit are loading
+
+  // ---- static first item: slot blockIdx.x of the split-major numbering ----
+  int cb = (int)(blockIdx.x % (unsigned)B);
+  int cs = (int)(blockIdx.x / (unsigned)B);
+  int cL;
+  {
+    // Page ids and the length leave together; the ids are masked to the
+    // split once the length is known.
+    const int start = cs * S;
+    const int spec = min(S / kPage, p.bt_pages - start / kPage);
+    int v = -1;
+    if (lane < spec) v = p.bt[(int64_t)cb * p.bt_srow + start / kPage + lane];
+    cL = clamped_len(p, cb);
+    if (cs < splits_of_len(cL, S)) {
+      const int tiles = max(0, (min(start + S, cL) - start + kPage - 1) / kPage);
+      pidU = (lane < tiles && v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
+      const int nU = (tiles + 1) >> 1;
+      if (nU > 0) load_block(buf[0], pidU, wave, 0);
+      if (nU > 1) load_block(buf[1], pidU, wave, 1);
+      issuedU = min(nU, 2);
+      load_q(cb, wave, qop);
+      u_loaded = true;
+    } else {
+      cb = -2;  // hole: the workgroup starts on the queue
+    }
   }
 
-  // The first item of workgroup w is item w; later items are claimed from the
-  // queue, one claim ahead: the claim for the next item is issued when the
-  // current one starts and only read when it ends, so its latency overlaps
-  // the work and the claims of different workgroups spread out in time.
-  int item = blockIdx.x;
-  while (item < total) {
-    unsigned int next_claim = 0;
-    if (threadIdx.x == 0) next_claim = gridDim.x + atomicAdd(&g_pd_queue[0], 1u);
-    int rb, split;
-    if (compact) {
-      int lo = 0, hi = B - 1;  // last b with s_prefix[b] <= item
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (lds_uniform(s_prefix, mid) <= item)
-          lo = mid;
-        else
-          hi = mid - 1;
-      }
-      rb = lo;
-      split = item - lds_uniform(s_prefix, rb);
-    } else {
-      rb = item / p.num_splits;
-      split = item - rb * p.num_splits;
-    }
-    const int L = compact ? lds_uniform(s_len, rb) : clamped_len(p, rb);
-    const int n_b = splits_of_len(L, S);
-    if (split < n_b) {  // false only for the fallback numbering; uniform over the workgroup
-    const int s_last = split;
-    const bool direct = n_b == 1;
-    const bool has_ws = p.num_splits > 1;
+  if (threadIdx.x == 0) {
+    s_seq[0] = -1;
+    s_seq[1] = -1;
+    s_ack[0] = nwaves - 1;  // both slots start out consumed
+    s_ack[1] = nwaves - 1;
+    s_prefix_ready = 0;
+  }
+  __syncthreads();
 
-    for (int kvh = wave; kvh < p.num_kv_heads; kvh += nwaves) {
-      if (L <= 0) {
-        // Empty sequence: zero output and -inf LSE for this head's rows.
-        for (int idx = lane; idx < mcols * D; idx += 64) {
-          const int col = idx / D;
-          const int d = idx - col * D;
-          const int g = col / q_len;
-          const int i = col - g * q_len;
-          const int64_t row = (int64_t)rb * q_len + i;
-          const int64_t h = (int64_t)kvh * p.group + g;
-          reinterpret_cast<QT *>(p.out)[row * p.o_srow + h * p.o_shead + d] = from_f32<QT>(0.0f);
-          if (d == 0 && p.lse) p.lse[row * p.lse_srow + h * p.lse_shead] = -INFINITY;
-        }
-        continue;
+  // ---- the queue (wave 0 only) ----
+  // Compact mode: s_prefix / s_len, built by the last wave while its first
+  // blocks load and read only by wave 0, which waits for s_prefix_ready
+  // before its first decode.
+  auto build_prefix = [&]() {
+    const int per = (B + 63) >> 6;  // sequences per lane, <= 64
+    int sum = 0;
+    for (int e0 = 0; e0 < per; e0 += 8) {
+      int lv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = lane * per + e0 + e;
+        lv[e] = (e0 + e < per && idx < B) ? p.seq_lens[idx] : 0;
       }
-      const int b = rb;
-      const int split_start = split * S;                      // run's first token
-      const int split_end = min((s_last + 1) * S, L);          // run's end token
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = lane * per + e0 + e;
+        if (e0 + e < per && idx < B) {
+          const int L = max(0, min(lv[e], p.l_cap));
+          s_len[idx] = L;
+          sum += max(0, splits_of_len(L, S) - static_splits(idx, G, B));
+        }
+      }
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    int run = incl - sum;
+    for (int e = 0; e < per; ++e) {
+      const int idx = lane * per + e;
+      if (idx < B) {
+        run += max(0, splits_of_len(s_len[idx], S) - static_splits(idx, G, B));
+        s_prefix[idx + 1] = run;
+      }
+    }
+    if (lane == 0) s_prefix[0] = 0;
+  };
+  auto queue_total = [&]() -> int64_t {
+    if (compact) return lds_uniform(s_prefix, B);
+    return max((int64_t)0, (int64_t)B * p.num_splits - G);
+  };
+  // Queue index -> item (b, s, L); false for a hole of the split-major numbering.
+  int db = -1, ds = 0, dL = 0;
+  auto decode = [&](int64_t c) {
+    if (compact) {
+      // Last b with s_prefix[b] <= c (the prefix is non-decreasing and
+      // s_prefix[0] = 0): two ballot rounds, chunks of ceil(B / 64).
+      const int ci = (int)c;
+      const int chunk = (B + 63) >> 6;
+      int idx = lane * chunk;
+      const uint64_t m1 = __ballot(idx < B && s_prefix[idx] <= ci);
+      const int base = (__popcll(m1) - 1) * chunk;
+      idx = base + lane;
+      const uint64_t m2 = __ballot(lane < chunk && idx < B && s_prefix[idx] <= ci);
+      const int b = base + __popcll(m2) - 1;
+      db = b;
+      ds = static_splits(b, G, B) + (ci - lds_uniform(s_prefix, b));
+      dL = lds_uniform(s_len, b);
+      return true;
+    }
+    const int64_t slot = (int64_t)G + c;
+    const int b = (int)(slot % B);
+    const int s = (int)(slot / B);
+    const int L = clamped_len(p, b);
+    if (s >= splits_of_len(L, S)) return false;
+    db = b;
+    ds = s;
+    dL = L;
+    return true;
+  };
+
+  // ---- next-item hand-off ----
+  // Item t's successor is claimed by wave 0 late in its last unit (claim
+  // point) and resolved and published in LDS slot t & 1 a few blocks later
+  // (checkpoint).  The other waves poll the slot from their own checkpoint
+  // on and wait for it only when they need the successor's page ids (two
+  // blocks before their unit ends); they then start prefetching it.  No
+  // barrier separates items: each reader acknowledges the slot, and wave 0
+  // rewrites a slot only after every other wave has acknowledged it.
+  unsigned int claim = 0;
+  bool claimed = false;  // wave 0: a claim is in flight
+  bool more = true;      // wave 0: the queue may still hold items
+  int t_item = 0;
+  int nb = -1, ns = 0, nL = 0;
+  auto issue_claim = [&]() {
+    if (lane == 0) claim = atomicAdd(&g_pd_queue[0], 1u);
+    claimed = true;
+  };
+  auto claim_point = [&]() {
+    if (wave == 0 && more && !claimed) issue_claim();
+  };
+  // Wave 0: the next item into (db, ds, dL); db = -1 when none is left.
+  auto resolve = [&]() {
+    db = -1;
+    if (!more) return;
+    if (!claimed) issue_claim();
+    if (compact)
+      while (!__builtin_amdgcn_readfirstlane(s_prefix_ready)) __builtin_amdgcn_s_sleep(1);
+    const int64_t Q = queue_total();
+    for (;;) {
+      const int64_t c = __builtin_amdgcn_readfirstlane(claim);
+      claimed = false;
+      if (c >= Q) {
+        more = false;
+        return;
+      }
+      if (decode(c)) return;
+      issue_claim();  // a hole of the split-major numbering
+    }
+  };
+  // Returns true once (nb, ns, nL) holds item t_item's successor.  Wave 0
+  // always completes; another wave returns false when `wait` is unset and
+  // the slot is not published yet.
+  auto checkpoint = [&](bool wait) {
+    const int slot = t_item & 1;
+    if (wave == 0) {
+      resolve();
+      while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(&s_ack[slot], __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_WORKGROUP)) < nwaves - 1)
+        __builtin_amdgcn_s_sleep(1);
+      if (lane == 0) {
+        __hip_atomic_store(&s_ack[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the reset ahead of the publication
+        s_pub[slot][0] = db;
+        s_pub[slot][1] = ds;
+        s_pub[slot][2] = dL;
+        s_seq[slot] = t_item;  // after the item fields (LDS operations of a wave execute in order)
+      }
+      nb = db;
+      ns = ds;
+      nL = dL;
+      return true;
+    }
+    while (__builtin_amdgcn_readfirstlane(s_seq[slot]) != t_item) {
+      if (!wait) return false;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    nb = __builtin_amdgcn_readfirstlane(s_pub[slot][0]);
+    ns = __builtin_amdgcn_readfirstlane(s_pub[slot][1]);
+    nL = __builtin_amdgcn_readfirstlane(s_pub[slot][2]);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // acknowledge only after the reads
+    if (lane == 0) __hip_atomic_fetch_add(&s_ack[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return true;
+  };
+
+  if (compact && wave == nwaves - 1) {
+    build_prefix();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the flag follows the table (LDS operations of a wave execute in order)
+    if (lane == 0) s_prefix_ready = 1;
+  }
+
+  int hh = 0;
+  while (cb != -1) {
+    if (cb < 0) checkpoint(true);  // the static item was a hole
+    if (cb >= 0) {
+      const int kvh = wave + nwaves * hh;
+      const int b = cb;
+      const int L = cL;
+      const int split = cs;
+      const int uStart = split * S;
+      const int uEnd = min(uStart + S, L);
+      const int nU = n_blocks(split, L);
+      const int n_b = splits_of_len(L, S);
+      const bool direct = n_b == 1;
+      const bool has_ws = p.num_splits > 1;
+      const bool last = hh + 1 == hpw;  // the item's successor follows this unit
+      if (!u_loaded) {
+        pidU = load_pid(b, split, L);
+        load_q(b, kvh, qop);
+        issuedU = 0;
+      }
+      // top up the unit's first two blocks
+      if (issuedU < 1 && nU > 0) {
+        if (par) load_block(buf[1], pidU, kvh, 0);
+        else load_block(buf[0], pidU, kvh, 0);
+      }
+      if (issuedU < 2 && nU > 1) {
+        if (par) load_block(buf[0], pidU, kvh, 1);
+        else load_block(buf[1], pidU, kvh, 1);
+      }
+
+      // ---- the next unit of this wave ----
+      bool hasN = false;
+      int nKvh = 0, nB = 0, nN = 0, pidN = -1;
+      int issuedN = 0;
+      auto set_next = [&]() {
+        if (!last) {
+          hasN = true;
+          nB = b;
+          nKvh = kvh + nwaves;
+          nN = nU;
+          pidN = pidU;
+        } else if (nb >= 0) {
+          hasN = true;
+          nB = nb;
+          nKvh = wave;
+          nN = n_blocks(ns, nL);
+          pidN = load_pid(nb, ns, nL);
+        }
+        if constexpr (kQPrefetch)
+          if (hasN) load_q(nB, nKvh, qopN);
+      };
+      // In the last unit the successor is claimed kClaimLead blocks and
+      // published kPublishLead blocks before the end (at the start of a
+      // shorter unit); the first blocks of N leave two blocks before the end.
+      const int k_claim = last ? nU - kClaimLead : -1;
+      const int k_pub = last ? nU - kPublishLead : -1;
+      bool n_ready = !last;
+      if (last) {
+        if (k_claim < 0) claim_point();
+        if (k_pub < 0) n_ready = checkpoint(true);
+      }
+      if (n_ready) set_next();
+
       const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
       const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
       const float c_log2 = k_scale * p.qk_scale_log2;
-
       // ---- masking limits: last visible token for this lane's column ----
       int lim[NQT];
 #pragma unroll
       for (int qt = 0; qt < NQT; ++qt) {
         const int col = 16 * qt + n16;
-        lim[qt] = min(split_end - 1, L - q_len + (col % q_len));
+        lim[qt] = min(uEnd - 1, L - q_len + (col % q_len));
       }
-      // The query operand is loaded after the first K/V loads are issued (the
-      // page-id -> K/V chain is the critical path at the start of a run).
-      qvec8 qop[NQT][NS];
-      const int min_lim = min(split_end - 1, L - q_len);
-
-      // ---- page ids of the split: lane t -> tile t (a split has <= 64 tiles) ----
-      const int tiles = (split_end - split_start + kPage - 1) / kPage;
-      const int nblk = (tiles + 1) >> 1;
-      int pid = -1;
-      if (lane < tiles) {
-        const int v = p.bt[(int64_t)b * p.bt_srow + split_start / kPage + lane];
-        pid = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
-      }
-
-      // Lane offsets inside a page fit in 32 bits (checked on the host), so the
-      // loads take the (uniform 64-bit page base + 32-bit lane offset) form.
-      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
-      const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
+      const int min_lim = min(uEnd - 1, L - q_len);
 
       f32x4 acc[NQT][NT];
       float m_run[NQT], l_run[NQT];
@@ -355,49 +636,20 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 
-      // Raw buffer loads through a per-page resource: the page base lives in
-      // SGPRs, one 32-bit lane offset serves every K (V) load of the page and
-      // the hardware range check (the page's byte extent) returns zeros for
-      // anything outside it.  Loads are unconditional -- an invalid page id
-      // reads page 0 -- and compute_block zeroes V of every token outside
-      // the split or on an invalid page.
-      auto load_block = [&](BlockRaw<D> &r, int blk) {
-#pragma unroll
-        for (int T = 0; T < 2; ++T) {
-          const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
-          const int page = raw_page >= 0 ? raw_page : 0;
-          const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-              const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
-#pragma unroll
-          for (int c = 0; c < NCH; ++c)
-            r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, 0));
-          const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-              const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if constexpr (D == 128)
-              r.v[4 * T + e] =
-                  __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, 0));
-            else
-              r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, 0);
-          }
-        }
-      };
-
       auto compute_block = [&](BlockRaw<D> &r, int blk) {
-        const int tok0 = split_start + 32 * blk;
+        const int tok0 = uStart + 32 * blk;
         // Tokens past the split (the tail of the sequence's last page, or a
         // tile beyond the split read from page 0) and tokens of an invalid
         // page may hold arbitrary bytes, NaN codes included: zero their V so
         // that p = 0 contributes exactly 0.  K needs no fix-up: their scores
         // are replaced by -inf below.
-        const bool bad0 = __builtin_amdgcn_readlane(pid, 2 * blk) < 0;
-        const bool bad1 = __builtin_amdgcn_readlane(pid, 2 * blk + 1) < 0;
-        if (tok0 + 32 > split_end || bad0 || bad1) {
+        const bool bad0 = __builtin_amdgcn_readlane(pidU, 2 * blk) < 0;
+        const bool bad1 = __builtin_amdgcn_readlane(pidU, 2 * blk + 1) < 0;
+        if (tok0 + 32 > uEnd || bad0 || bad1) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-            if (t >= split_end || ((e >> 2) ? bad1 : bad0)) {
+            if (t >= uEnd || ((e >> 2) ? bad1 : bad0)) {
               if constexpr (D == 128)
                 r.v[e] = i32x2{0, 0};
               else
@@ -469,21 +721,21 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         }
         // ---- O^T += V^T . P^T ----
 #pragma unroll
-        for (int tp = 0; tp < NT; tp += 2) {
-          // d tiles tp, tp+1 use byte pair (tp % 4, tp % 4 + 1) of dword tp / 4
+        for (int tp2 = 0; tp2 < NT; tp2 += 2) {
+          // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
           i32x4 wa, wb;
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
             int w0, w1;
             if constexpr (D == 128) {
-              w0 = r.v[e][tp >> 2];
-              w1 = r.v[e + 1][tp >> 2];
+              w0 = r.v[e][tp2 >> 2];
+              w1 = r.v[e + 1][tp2 >> 2];
             } else {
               w0 = r.v[e];
               w1 = r.v[e + 1];
             }
-            const f32x2 f0 = fp8x2_f32(w0, (tp & 3) != 0);
-            const f32x2 f1 = fp8x2_f32(w1, (tp & 3) != 0);
+            const f32x2 f0 = fp8x2_f32(w0, (tp2 & 3) != 0);
+            const f32x2 f1 = fp8x2_f32(w1, (tp2 & 3) != 0);
             wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
             wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
           }
@@ -491,49 +743,46 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           const f16x8 vb = __builtin_bit_cast(f16x8, wb);
 #pragma unroll
           for (int qt = 0; qt < NQT; ++qt) {
-            acc[qt][tp] = mfma16(va, pop[qt], acc[qt][tp]);
-            acc[qt][tp + 1] = mfma16(vb, pop[qt], acc[qt][tp + 1]);
+            acc[qt][tp2] = mfma16(va, pop[qt], acc[qt][tp2]);
+            acc[qt][tp2 + 1] = mfma16(vb, pop[qt], acc[qt][tp2 + 1]);
           }
         }
       };
 
-      // ---- main loop: the split's 32-token blocks through kDepth register buffers ----
-      // Block k is computed while blocks k+1 .. k+kDepth-1 are in flight; its
-      // buffer is refilled with block k+kDepth right after.
+      // Compute block k, then refill its buffer with stream position k + 2:
+      // the unit's own block or, in order, the next unit's first two blocks.
+      auto step = [&](BlockRaw<D> &r, int k) {
+        compute_block(r, k);
+        const int pos = k + 2;
+        if (pos < nU) {
+          load_block(r, pidU, kvh, pos);
+        } else if (pos - nU == issuedN && issuedN < nN) {
+          load_block(r, pidN, nKvh, issuedN);
+          ++issuedN;
+        }
+        if (k == k_claim) claim_point();
+        // From the checkpoint on, poll for the successor; wait for it
+        // kNeedLead blocks before the end (its first block is the refill
+        // after the next).
+        if (!n_ready && k >= k_pub) {
+          n_ready = checkpoint(k + kNeedLead >= nU);
+          if (n_ready) set_next();
+        }
+      };
       {
-        BlockRaw<D> buf[kDepth];
-#pragma unroll
-        for (int i = 0; i < kDepth; ++i)
-          if (i < nblk) load_block(buf[i], i);
-        // ---- query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16 ----
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-          const int col = 16 * qt + n16;
-          const int g = col / q_len;
-          const int i = col - g * q_len;
-          if (col < mcols) {
-            const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
-                             (int64_t)(kvh * p.group + g) * p.q_shead;
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-              const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
-              qop[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
-            }
-          } else {
-#pragma unroll
-            for (int s = 0; s < NS; ++s) qop[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
-          }
+        int k = 0;
+        if (par && nU > 0) {
+          step(buf[1], 0);
+          k = 1;
         }
-        for (int k = 0; k < nblk; k += kDepth) {
-#pragma unroll
-          for (int i = 0; i < kDepth; ++i) {
-            if (k + i < nblk) {
-              compute_block(buf[i], k + i);
-              if (k + i + kDepth < nblk) load_block(buf[i], k + i + kDepth);
-            }
-          }
+        for (; k + 1 < nU; k += 2) {
+          step(buf[0], k);
+          step(buf[1], k + 1);
         }
+        if (k < nU) step(buf[0], k);
       }
+      if constexpr (!kQPrefetch)
+        if (hasN) load_q(nB, nKvh, qop);  // qop is dead once the last block is computed
 
       // ---- epilogue: this lane holds column 16*qt + lane%16, dims [DPL*j, DPL*j + DPL) ----
 #pragma unroll
@@ -603,16 +852,34 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           }
         }
       }
+
+      // ---- the next unit inherits the stream ----
+      par = (par + nU) & 1;
+      pidU = pidN;
+      issuedU = issuedN;
+      u_loaded = hasN;
+      if constexpr (kQPrefetch) {
+        if (hasN) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) qop[0][s] = qopN[0][s];
+        }
+      }
+      if (hh + 1 < hpw) {
+        ++hh;
+        continue;
+      }
     }
-    }  // split < n_b
-    if (threadIdx.x == 0) s_item = (int)next_claim;
-    __syncthreads();
-    item = __builtin_amdgcn_readfirstlane(s_item);
-    __syncthreads();  // s_item is rewritten by the next claim
+    // ---- item transition (no barrier: see the hand-off above) ----
+    hh = 0;
+    cb = nb;
+    cs = ns;
+    cL = nL;
+    ++t_item;
   }
   // ---- end of the launch: the last workgroup out resets the queue ----
-  // No fence: the counters order nothing else, and the kernel boundary
-  // publishes the reset (a fence here would write back the XCD's L2).
+  // Every claim of this workgroup has been resolved by now.  No fence: the
+  // counters order nothing else, and the kernel boundary publishes the reset
+  // (a fence here would write back the XCD's L2).
   if (threadIdx.x == 0) {
     const unsigned int done = atomicAdd(&g_pd_queue[1], 1u);
     if (done == gridDim.x - 1) {
@@ -878,34 +1145,56 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   return L20_PD_OK;
 }
 
+// Waves per partial workgroup: the largest divisor of the KV head count
+// that is at most kMaxWaves, so every wave owns the same number of heads.
+int partial_waves(int num_kv_heads) {
+  for (int w = std::min(num_kv_heads, l20pd::kMaxWaves); w > 1; --w)
+    if (num_kv_heads % w == 0) return w;
+  return 1;
+}
+
+// Compact item numbering needs the batch's prefix in LDS.
+bool partial_compact(int batch) { return batch <= l20pd::kMaxCompactBatch; }
+
 // Workgroups the persistent partial kernel launches: enough to fill every CU
-// at the kernel's occupancy, never more than there can be work items.
+// at the kernel's occupancy, never more than there are split-major slots.
+// L20_PD_MAX_WORKGROUPS (a positive integer) caps the count, which lets tests
+// drive many items through each workgroup.
 template <typename QT, int D, int NQT>
-int partial_grid(int threads, int64_t max_items) {
+int partial_grid(int threads, size_t lds, int64_t max_items) {
   static thread_local int cached_dev = -1, cached_threads = -1, cached_blocks = 0;
+  static thread_local size_t cached_lds = 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  if (dev != cached_dev || threads != cached_threads) {
+  if (dev != cached_dev || threads != cached_threads || lds != cached_lds) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, D, NQT>, threads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, D, NQT>, threads, lds) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
     cached_dev = dev;
     cached_threads = threads;
+    cached_lds = lds;
     cached_blocks = cus * per_cu;
   }
-  return (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, max_items));
+  int64_t blocks = cached_blocks;
+  if (const char *cap = getenv("L20_PD_MAX_WORKGROUPS")) {
+    const long v = strtol(cap, nullptr, 10);
+    if (v > 0) blocks = std::min<int64_t>(blocks, v);
+  }
+  return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, max_items));
 }
 
 template <typename QT, int D, int NQT>
-hipError_t launch_partial(const l20pd::PartialParams &pp, int batch, int num_kv_heads, hipStream_t stream) {
-  const int nwaves = std::min(num_kv_heads, l20pd::kMaxWaves);
+hipError_t launch_partial(l20pd::PartialParams pp, int batch, int num_kv_heads, hipStream_t stream) {
+  const int nwaves = partial_waves(num_kv_heads);
   const int threads = 64 * nwaves;
+  pp.compact = partial_compact(batch) ? 1 : 0;
+  const size_t lds = pp.compact ? (size_t)(2 * batch + 1) * sizeof(int) : 0;
   const int64_t max_items = (int64_t)batch * pp.num_splits;
-  const int grid = partial_grid<QT, D, NQT>(threads, max_items);
-  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), dim3(grid), dim3(threads), 0, stream, pp);
+  const int grid = partial_grid<QT, D, NQT>(threads, lds, max_items);
+  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), dim3(grid), dim3(threads), lds, stream, pp);
   return hipGetLastError();
 }
 
@@ -971,6 +1260,7 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   const int64_t cap = std::min<int64_t>((int64_t)pp.num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
   pp.l_cap = (int)cap;
   pp.batch = a.batch;
+  pp.bt_pages = a.bt_max_pages;
   return pp;
 }
 
@@ -1075,20 +1365,18 @@ int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args) {
 }
 
 int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len, int32_t cu_count) {
-  if (cu_count <= 0) cu_count = 256;
-  const int64_t units = (int64_t)(batch > 0 ? batch : 1) * (num_kv_heads > 0 ? num_kv_heads : 1);
-  // Aim for >= 2 work items per CU; larger splits amortise the partial
-  // round trip, so take the largest split that still reaches that count.
-  const int64_t target = 2 * (int64_t)cu_count;
-  int32_t best = 64;
-  for (int32_t s = 1024; s >= 64; s -= 64) {
-    const int64_t items = units * (int64_t)l20_pd_num_splits(max_seq_len > 0 ? max_seq_len : 1, s);
-    if (items >= target) {
-      best = s;
-      break;
-    }
-  }
-  return best;
+  // Measured on MI355X over the benchmark workloads: 512-token splits (the
+  // reference hook's default) for ragged serving batches, 1024 for long
+  // contexts (fewer partials to merge), and at least ~8 splits per sequence
+  // for short contexts, where the launch is latency-bound.  The batch, head
+  // and CU counts are part of the signature for future heuristics.
+  (void)batch;
+  (void)num_kv_heads;
+  (void)cu_count;
+  if (max_seq_len > 32768) return 1024;
+  int32_t s = 512;
+  while (s > 64 && (int64_t)s * 8 > max_seq_len) s >>= 1;
+  return s;
 }
 
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth); }

@@ -48,8 +48,12 @@ def test_num_splits_and_default_split_size():
     for b, h, s in [(128, 4, 8192), (2, 8, 131072), (4, 2, 512), (1, 1, 16)]:
         split = lib.l20_pd_default_split_size(b, h, s, 256)
         assert 64 <= split <= 1024 and split % 16 == 0
-    # long single sequences get the largest split that still fills the chip
+    # long contexts take the largest split; serving batches the hook's 512;
+    # short contexts keep ~8 splits per sequence
     assert lib.l20_pd_default_split_size(2, 8, 131072, 256) == 1024
+    assert lib.l20_pd_default_split_size(128, 4, 8192, 256) == 512
+    assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 256
+    assert lib.l20_pd_default_split_size(4, 2, 512, 256) == 64
 
 
 def valid_args():

@@ -209,3 +209,33 @@ def test_hip_graph_capture_replays_match_eager():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager_out) and torch.equal(lse, eager_lse)
+
+
+# ------------------------------------------------------------ work queue
+# L20_PD_MAX_WORKGROUPS caps the persistent grid, so each workgroup streams
+# many items (and unit-to-unit prefetch crosses items of different sequences).
+QUEUE = [
+    # name, batch, hq, hkv, d, lens, q_len, split
+    ("compact_ragged", 8, 16, 2, 128, [3000, 0, 17, 700, 64, 1, 2049, 333], 1, 64),
+    ("two_heads_per_wave", 3, 24, 12, 128, [900, 31, 400], 1, 128),
+    ("three_heads_per_wave_d64", 2, 18, 9, 64, [500, 77], 1, 64),
+    ("verify_q4", 4, 16, 2, 128, [700, 4, 130, 1500], 4, 96),
+    # more sequences than the LDS prefix holds: split-major numbering with holes
+    ("split_major_fallback", 600, 4, 1, 64, None, 1, 64),
+]
+
+
+@pytest.mark.parametrize("case", QUEUE, ids=[c[0] for c in QUEUE])
+@pytest.mark.parametrize("max_wg", [1, 3, 0])
+def test_work_queue_small_grids(case, max_wg, monkeypatch):
+    name, batch, hq, hkv, d, lens, q_len, split = case
+    if lens is None:
+        lens = np.random.default_rng(11).integers(0, 200, size=batch).tolist()
+        lens[5] = 0
+    if max_wg:
+        monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", str(max_wg))
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, seed=zlib.crc32(name.encode()) % 1000,
+                           garbage_tail=True)
+    exp = H.run_oracle(inp)
+    for _ in range(2):  # the queue counters reset themselves between launches
+        H.compare(*H.run_op(inp, split), *exp)
