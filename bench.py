@@ -86,6 +86,23 @@ def cpu_baseline(inp, cfg, sample_seqs):
     }
 
 
+def measured_traffic(workload: str, split: int, kernel: str = "pd_fp8_partial"):
+    """HBM bytes per launch of ``kernel`` from the committed counter profile
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE passes scaled by a copy of known size),
+    or None when the profile has no entry for this workload and split."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    for e in data["entries"]:
+        if e["workload"] == workload and e["split_size"] == split and e["kernel"] == kernel:
+            read = e["fetch_kib"] * 1024 * data["fetch_scale"]
+            write = e["write_kib"] * 1024 * data["write_scale"]
+            return {"bytes": int(read + write), "read_bytes": int(read), "write_bytes": int(write),
+                    "source": data["source"]}
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -177,6 +194,7 @@ def main():
         sample = args.cpu_sample or min(cfg.batch, 32)
         cpu = cpu_baseline(first, cfg, sample)
 
+    traffic = measured_traffic(cfg.name, split)
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -214,7 +232,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_detail": traffic,
             "partial_us_mean": round(partial_mean_ms * 1e3, 2),
             "partial_us_p10_p90": [round(sorted(partial_ms)[len(partial_ms) // 10] * 1e3, 2),
                                    round(sorted(partial_ms)[(9 * len(partial_ms)) // 10] * 1e3, 2)],
