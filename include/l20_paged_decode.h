@@ -21,6 +21,12 @@
  *                              <- fp8x2_e4m3fn_to_float2, l20_paged_decode.cu:20-33
  *                                 (the device-side e4m3fn conversion, exposed as a
  *                                 bulk dequantiser)
+ *   l20_pd_split_out           <- l20_paged_decode_split_out_cuda (fp16 caches,
+ *                                 l20_paged_decode.cu:549-597, TORCH_LIBRARY schema at
+ *                                 l20_paged_decode.cpp:121-127) and
+ *                                 l20_paged_decode_split_indices_out_cuda (CSR page
+ *                                 lists, l20_paged_decode.cu:600-649, pybind export at
+ *                                 l20_paged_decode.cpp:150-152)
  */
 #ifndef L20_PAGED_DECODE_H_
 #define L20_PAGED_DECODE_H_
@@ -32,13 +38,20 @@
 extern "C" {
 #endif
 
-#define L20_PD_ABI_VERSION 1
+#define L20_PD_ABI_VERSION 2
 
 /* Element types for query/output and the partial-output workspace. */
 enum l20_pd_dtype {
   L20_PD_BF16 = 0,
   L20_PD_FP16 = 1,
   L20_PD_FP32 = 2
+};
+
+/* Element types of the K/V caches. */
+enum l20_pd_kv_dtype {
+  L20_PD_KV_FP8_E4M3 = 0,  /* OCP e4m3fn codes, dequantised as code * scale */
+  L20_PD_KV_FP16 = 1,      /* fp16 values (query must be fp16) */
+  L20_PD_KV_BF16 = 2       /* bf16 values (query must be bf16) */
 };
 
 /* Return codes. */
@@ -55,7 +68,9 @@ enum l20_pd_status {
  *
  *   query          [batch*q_len, num_q_heads, head_dim]   bf16 or fp16
  *   key/value      [num_pages, page_size=16, num_kv_heads, head_dim]  e4m3fn bytes
- *   block_table    [batch, >= ceil(max_seq_len/16)]  int32 physical page ids
+ *   block_table    [batch, >= ceil(max_seq_len/16)]  int32 physical page ids, or,
+ *                  with page_indptr [batch+1] (CSR), the flat page list: sequence b's
+ *                  pages are block_table[page_indptr[b] .. page_indptr[b+1])
  *   seq_lens       [batch]  int32, each <= max_seq_len, includes the q_len new tokens
  *   partial_output [batch*q_len, num_q_heads, >= num_splits, head_dim]  fp32 or fp16
  *   partial_max/sum[batch*q_len, num_q_heads, >= num_splits]  fp32
@@ -67,7 +82,9 @@ enum l20_pd_status {
  * code * scale with the per-head scale arrays (fp32 [num_kv_heads], device
  * memory) when non-NULL, else with the scalar scales.  softmax_scale <= 0
  * selects head_dim^-0.5.  The contents of the partial workspace after a call
- * are unspecified.
+ * are unspecified.  kv_dtype selects the cache element type (strides of
+ * 16-bit caches are in elements, like every other tensor); a zero-initialised
+ * struct describes fp8 caches addressed through a block table.
  */
 typedef struct l20_pd_fp8_args {
   const void *query;
@@ -107,6 +124,10 @@ typedef struct l20_pd_fp8_args {
 
   int32_t batch, q_len, num_q_heads, num_kv_heads, head_dim;
   int32_t max_seq_len, split_size;
+
+  /* ABI version 2 */
+  int32_t kv_dtype;                /* enum l20_pd_kv_dtype */
+  const int32_t *page_indptr;      /* CSR row offsets [batch+1], or NULL for block_table rows */
 } l20_pd_fp8_args;
 
 /* ABI version of the loaded library (L20_PD_ABI_VERSION). */
@@ -123,8 +144,15 @@ int32_t l20_pd_num_splits(int32_t max_seq_len, int32_t split_size);
 int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args);
 
 /* Enqueue the split-KV partial kernel and the LSE merge kernel on `stream`
- * (hipStream_t, NULL = default stream).  Asynchronous; allocates nothing. */
+ * (hipStream_t, NULL = default stream).  Asynchronous; allocates nothing.
+ * Requires kv_dtype == L20_PD_KV_FP8_E4M3. */
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
+
+/* The fp16/bf16-KV sibling: the same two kernels over 16-bit caches
+ * (kv_dtype L20_PD_KV_FP16 or L20_PD_KV_BF16, query of the same type; the
+ * scalar/per-head scales still multiply K and V, 1.0 reproduces the
+ * reference).  With page_indptr set it is the CSR variant. */
+int32_t l20_pd_split_out(const l20_pd_fp8_args *args, void *stream);
 
 /* The two stages of l20_pd_fp8_e4m3_split_out, enqueued separately (same
  * arguments, same validation): the split-KV partial kernel

@@ -169,6 +169,43 @@ def dequantize(codes: np.ndarray, scale: ScaleLike, head_axis: int = -2) -> np.n
     return (values * scales.reshape(shape)).astype(np.float32)
 
 
+def table_row(block_table: np.ndarray, b: int, page_indptr: Optional[np.ndarray] = None) -> np.ndarray:
+    """Page list of sequence ``b``: row ``b`` of a ``[B, max_pages]`` block table, or
+    ``page_indices[indptr[b]:indptr[b+1]]`` of a CSR page list
+    (``l20_paged_decode.cu:205-208``: ``page_indptr[batch] + logical_page``)."""
+    if page_indptr is None:
+        return np.asarray(block_table[b])
+    return np.asarray(block_table)[int(page_indptr[b]):int(page_indptr[b + 1])]
+
+
+def _attend(query_rows: np.ndarray, keys: np.ndarray, values: np.ndarray, num_kv_heads: int,
+            scale: float, q_len: int, acc_dtype) -> Tuple[np.ndarray, np.ndarray]:
+    """Softmax attention of one sequence's ``q_len`` query rows over its ``L`` keys;
+    row ``i`` sees keys ``0 .. L - q_len + i``.  Returns (out [q, Hq, D], lse [q, Hq])."""
+    length = keys.shape[0]
+    _, num_q_heads, head_dim = query_rows.shape
+    group = num_q_heads // num_kv_heads
+    keys = keys.astype(acc_dtype)
+    values = values.astype(acc_dtype)
+    # [q, Hkv, G, D] x [L, Hkv, D] -> [q, Hkv, G, L]
+    q = query_rows.reshape(q_len, num_kv_heads, group, head_dim)
+    scores = np.einsum("ihgd,thd->ihgt", q.astype(acc_dtype), keys) * acc_dtype(scale)
+    token = np.arange(length)
+    limit = length - q_len + np.arange(q_len)  # last visible key per row
+    visible = token[None, :] <= limit[:, None]  # [q, L]
+    scores = np.where(visible[:, None, None, :], scores, -np.inf)
+    row_max = scores.max(axis=-1, keepdims=True)
+    safe_max = np.where(np.isfinite(row_max), row_max, 0.0)
+    weights = np.exp(scores - safe_max)
+    denom = weights.sum(axis=-1, keepdims=True)
+    probs = np.divide(weights, denom, out=np.zeros_like(weights), where=denom > 0)
+    attended = np.einsum("ihgt,thd->ihgd", probs, values)
+    with np.errstate(divide="ignore"):
+        row_lse = (safe_max + np.log(denom))[..., 0]
+    row_lse = np.where(denom[..., 0] > 0, row_lse, -np.inf)
+    return attended.reshape(q_len, num_q_heads, head_dim), row_lse.reshape(q_len, num_q_heads)
+
+
 def reference(
     query: np.ndarray,
     key_cache: np.ndarray,
@@ -183,13 +220,14 @@ def reference(
     round_kv_to: Optional[np.dtype] = None,
     acc_dtype: np.dtype = np.float32,
     rows: Optional[Sequence[int]] = None,
+    page_indptr: Optional[np.ndarray] = None,
 ) -> Tuple[np.ndarray, np.ndarray]:
     """Dequantise-then-attend (``smoke_cuda_paged_fp8_decode_op.py:22-41``).
 
     query       [B*q_len, Hq, D] float (bf16/fp16 values held as float32)
     key/value   [P, 16, Hkv, D] uint8 e4m3fn codes
-    block_table [B, max_pages] int, seq_lens [B] int
-    k/v_scale   float or [Hkv]
+    block_table [B, max_pages] int (or the flat page list with ``page_indptr`` [B+1])
+    seq_lens    [B] int;  k/v_scale float or [Hkv]
     Row ``b*q_len + i`` attends to keys ``0 .. L_b - q_len + i``.
     Returns ``(out [B*q_len, Hq, D] float32, lse [B*q_len, Hq] float32)``;
     rows with no visible key give zeros and ``lse = -inf``.
@@ -199,7 +237,6 @@ def reference(
     n_rows, num_q_heads, head_dim = query.shape
     batch = n_rows // q_len
     num_kv_heads = key_cache.shape[2]
-    group = num_q_heads // num_kv_heads
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
     out = np.zeros((n_rows, num_q_heads, head_dim), dtype=np.float32)
     lse = np.full((n_rows, num_q_heads), -np.inf, dtype=np.float32)
@@ -207,31 +244,50 @@ def reference(
         length = int(seq_lens[b])
         if length <= 0:
             continue
-        keys = dequantize(gather_pages(key_cache, block_table[b], length), k_scale)
-        values = dequantize(gather_pages(value_cache, block_table[b], length), v_scale)
+        pages = table_row(block_table, b, page_indptr)
+        keys = dequantize(gather_pages(key_cache, pages, length), k_scale)
+        values = dequantize(gather_pages(value_cache, pages, length), v_scale)
         if round_kv_to is not None:
             keys = keys.astype(round_kv_to).astype(np.float32)
             values = values.astype(round_kv_to).astype(np.float32)
-        keys = keys.astype(acc_dtype)
-        values = values.astype(acc_dtype)
-        # [q, Hkv, G, D] x [L, Hkv, D] -> [q, Hkv, G, L]
-        q = query[b * q_len:(b + 1) * q_len].reshape(q_len, num_kv_heads, group, head_dim)
-        scores = np.einsum("ihgd,thd->ihgt", q.astype(acc_dtype), keys) * acc_dtype(scale)
-        token = np.arange(length)
-        limit = length - q_len + np.arange(q_len)  # last visible key per row
-        visible = token[None, :] <= limit[:, None]  # [q, L]
-        scores = np.where(visible[:, None, None, :], scores, -np.inf)
-        row_max = scores.max(axis=-1, keepdims=True)
-        safe_max = np.where(np.isfinite(row_max), row_max, 0.0)
-        weights = np.exp(scores - safe_max)
-        denom = weights.sum(axis=-1, keepdims=True)
-        probs = np.divide(weights, denom, out=np.zeros_like(weights), where=denom > 0)
-        attended = np.einsum("ihgt,thd->ihgd", probs, values)
-        out[b * q_len:(b + 1) * q_len] = attended.reshape(q_len, num_q_heads, head_dim)
-        with np.errstate(divide="ignore"):
-            row_lse = (safe_max + np.log(denom))[..., 0]
-        row_lse = np.where(denom[..., 0] > 0, row_lse, -np.inf)
-        lse[b * q_len:(b + 1) * q_len] = row_lse.reshape(q_len, num_q_heads)
+        o, l = _attend(query[b * q_len:(b + 1) * q_len], keys, values, num_kv_heads, scale, q_len, acc_dtype)
+        out[b * q_len:(b + 1) * q_len] = o
+        lse[b * q_len:(b + 1) * q_len] = l
+    return out, lse
+
+
+def reference_dense_kv(
+    query: np.ndarray,
+    key_cache: np.ndarray,
+    value_cache: np.ndarray,
+    block_table: np.ndarray,
+    seq_lens: np.ndarray,
+    *,
+    softmax_scale: Optional[float] = None,
+    q_len: int = 1,
+    rows: Optional[Sequence[int]] = None,
+    page_indptr: Optional[np.ndarray] = None,
+) -> Tuple[np.ndarray, np.ndarray]:
+    """The fp16/bf16-KV siblings (``smoke_cuda_paged_decode_op.py:13-29``,
+    ``l20_paged_decode.cu:156-289``): the same attention over caches whose values are
+    used as stored (fp16/bf16 values held as float32), no scales, fp32 accumulation."""
+    query = np.asarray(query, dtype=np.float32)
+    n_rows, num_q_heads, head_dim = query.shape
+    batch = n_rows // q_len
+    num_kv_heads = key_cache.shape[2]
+    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    out = np.zeros((n_rows, num_q_heads, head_dim), dtype=np.float32)
+    lse = np.full((n_rows, num_q_heads), -np.inf, dtype=np.float32)
+    for b in (range(batch) if rows is None else rows):
+        length = int(seq_lens[b])
+        if length <= 0:
+            continue
+        pages = table_row(block_table, b, page_indptr)
+        keys = np.asarray(gather_pages(key_cache, pages, length), dtype=np.float32)
+        values = np.asarray(gather_pages(value_cache, pages, length), dtype=np.float32)
+        o, l = _attend(query[b * q_len:(b + 1) * q_len], keys, values, num_kv_heads, scale, q_len, np.float32)
+        out[b * q_len:(b + 1) * q_len] = o
+        lse[b * q_len:(b + 1) * q_len] = l
     return out, lse
 
 

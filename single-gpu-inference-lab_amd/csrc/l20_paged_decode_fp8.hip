@@ -41,6 +41,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "l20_paged_decode.h"
 
@@ -98,7 +99,8 @@ struct PartialParams {
   int l_cap;  // min(num_splits * split_size, block-table pages * 16): tokens past it are never touched
   int batch;
   int bt_pages;  // block-table row length
-  int compact;   // queue items numbered through an LDS prefix (batch <= 8 * threads)
+  int compact;   // queue items numbered through an LDS prefix
+  const int32_t *indptr;  // CSR page list: sequence b's pages are bt[indptr[b] .. indptr[b + 1])
 };
 
 // ---------------------------------------------------------------------------
@@ -168,6 +170,21 @@ template <> struct BlockRaw<64> {
   i32x4 k[2][1];
   int v[8];       // 4 B at d = 4*(lane%16)
 };
+
+// Raw fp16/bf16 elements of one 16-token block (one page) held by one lane.
+template <int D> struct BlockRaw16;
+template <> struct BlockRaw16<128> {
+  i32x4 k[4];  // [k slice]: 8 elements at d = 64*(s/2) + 16*(lane/16) + 8*(s%2)
+  i32x4 v[4];  // [token slot]: 8 elements at d = 8*(lane%16)
+};
+template <> struct BlockRaw16<64> {
+  i32x4 k[2];
+  i32x2 v[4];  // 4 elements at d = 4*(lane%16)
+};
+// KT = 0: e4m3fn codes, 32-token blocks; KT = 1: 16-bit elements of the MFMA
+// type, 16-token blocks (the same bytes per register buffer).
+template <int KT, int D> struct KvBlock { typedef BlockRaw<D> type; };
+template <int D> struct KvBlock<1, D> { typedef BlockRaw16<D> type; };
 
 // ---------------------------------------------------------------------------
 // Partial kernel
@@ -250,9 +267,19 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // An item of a single-split sequence writes the final output and LSE (and
 // marks split slot 0 with +inf for the merge); any other item writes its
 // fp32 partial (o / l, m, l) at its split slot.
-template <typename QT, int D, int NQT>
+template <typename QT, int KT, int D, int NQT>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
+  typedef typename KvBlock<KT, D>::type Block;
+  // Softmax probabilities: f16 for fp8 caches (V converted to f16), the
+  // cache's own type for 16-bit caches.
+  typedef typename std::conditional<KT == 0, _Float16, QT>::type PT;
+  typedef typename MfmaTypes<PT>::vec8 pvec8;
+  constexpr int kTok = KT == 0 ? 32 : 16;  // tokens per block
+  // bf16 probabilities carry 8 significant bits: split P = hi + lo (both
+  // bf16) and accumulate both products, which restores ~16 bits.
+  constexpr bool kSplitP = KT == 1 && std::is_same<QT, __bf16>::value;
+  constexpr int kLeadMul = 32 / kTok;      // hand-off leads in 32-token units
   constexpr int NCH = D / 64;  // 64-byte K chunks per token row
   constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
   constexpr int NT = D / 16;   // 16-row d tiles of the PV product
@@ -287,16 +314,24 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   auto n_blocks = [&](int s, int L) {
     const int start = s * S;
     const int tiles = max(0, (min(start + S, L) - start + kPage - 1) / kPage);
-    return (tiles + 1) >> 1;
+    return KT == 0 ? (tiles + 1) >> 1 : tiles;
   };
+  // Sequence b's page list and its length (a block-table row, or the CSR
+  // slice; l20_paged_decode.cu:205-208).
+  auto row_of = [&](int b) -> const int32_t * {
+    return p.indptr ? p.bt + p.indptr[b] : p.bt + (int64_t)b * p.bt_srow;
+  };
+  auto pages_of = [&](int b) { return p.indptr ? p.indptr[b + 1] - p.indptr[b] : p.bt_pages; };
   // Page ids of split s of sequence b: lane t -> tile t (a split has <= 64
-  // tiles); -1 for tiles past the split and for out-of-range ids.
+  // tiles); -1 for tiles past the split, past the page list, and for
+  // out-of-range ids.
   auto load_pid = [&](int b, int s, int L) {
     const int start = s * S;
     const int tiles = max(0, (min(start + S, L) - start + kPage - 1) / kPage);
+    const int avail = pages_of(b) - start / kPage;
     int v = -1;
-    if (lane < tiles) {
-      v = p.bt[(int64_t)b * p.bt_srow + start / kPage + lane];
+    if (lane < tiles && lane < avail) {
+      v = row_of(b)[start / kPage + lane];
       v = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
     }
     return v;
@@ -329,7 +364,30 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // and compute_block zeroes V of every token outside the split or on an
   // invalid page.  Lane offsets inside a page fit in 32 bits (checked on the
   // host).
-  auto load_block = [&](BlockRaw<D> &r, int pid, int kvh, int blk) {
+  auto load_block = [&](Block &r, int pid, int kvh, int blk) {
+    if constexpr (KT == 1) {
+      // 16-bit elements: one page per block; K slice s at byte 128*(s/2) + 16*(s%2)
+      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 32 * j);
+      const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + 2 * (D / 16) * n16);
+      const int raw_page = __builtin_amdgcn_readlane(pid, blk);
+      const int page = raw_page >= 0 ? raw_page : 0;
+      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        r.k[s] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), 0));
+      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (D == 128)
+          r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, 0));
+        else
+          r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, 0));
+      }
+      return;
+    }
+    else {
     const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
     const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
 #pragma unroll
@@ -351,10 +409,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, 0);
       }
     }
+    }
   };
 
   // ---- stream state (wave-uniform except the VGPR operands) ----
-  BlockRaw<D> buf[2];
+  Block buf[2];
   qvec8 qop[NQT][NS];
   qvec8 qopN[kQPrefetch ? NQT : 1][NS];
   int pidU = -1;
@@ -370,14 +429,14 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     // Page ids and the length leave together; the ids are masked to the
     // split once the length is known.
     const int start = cs * S;
-    const int spec = min(S / kPage, p.bt_pages - start / kPage);
+    const int spec = min(S / kPage, pages_of(cb) - start / kPage);
     int v = -1;
-    if (lane < spec) v = p.bt[(int64_t)cb * p.bt_srow + start / kPage + lane];
+    if (lane < spec) v = row_of(cb)[start / kPage + lane];
     cL = clamped_len(p, cb);
     if (cs < splits_of_len(cL, S)) {
       const int tiles = max(0, (min(start + S, cL) - start + kPage - 1) / kPage);
-      pidU = (lane < tiles && v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
-      const int nU = (tiles + 1) >> 1;
+      pidU = (lane < tiles && lane < spec && v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
+      const int nU = KT == 0 ? (tiles + 1) >> 1 : tiles;
       if (nU > 0) load_block(buf[0], pidU, wave, 0);
       if (nU > 1) load_block(buf[1], pidU, wave, 1);
       issuedU = min(nU, 2);
@@ -605,8 +664,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // In the last unit the successor is claimed kClaimLead blocks and
       // published kPublishLead blocks before the end (at the start of a
       // shorter unit); the first blocks of N leave two blocks before the end.
-      const int k_claim = last ? nU - kClaimLead : -1;
-      const int k_pub = last ? nU - kPublishLead : -1;
+      const int k_claim = last ? nU - kClaimLead * kLeadMul : -1;
+      const int k_pub = last ? nU - kPublishLead * kLeadMul : -1;
       bool n_ready = !last;
       if (last) {
         if (k_claim < 0) claim_point();
@@ -636,24 +695,39 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 
-      auto compute_block = [&](BlockRaw<D> &r, int blk) {
-        const int tok0 = uStart + 32 * blk;
+      auto compute_block = [&](Block &r, int blk) {
+        const int tok0 = uStart + kTok * blk;
         // Tokens past the split (the tail of the sequence's last page, or a
         // tile beyond the split read from page 0) and tokens of an invalid
         // page may hold arbitrary bytes, NaN codes included: zero their V so
         // that p = 0 contributes exactly 0.  K needs no fix-up: their scores
-        // are replaced by -inf below.
-        const bool bad0 = __builtin_amdgcn_readlane(pidU, 2 * blk) < 0;
-        const bool bad1 = __builtin_amdgcn_readlane(pidU, 2 * blk + 1) < 0;
-        if (tok0 + 32 > uEnd || bad0 || bad1) {
+        // are replaced by -inf below.  A 16-bit block has one tile; its
+        // second-tile slots are empty (score -inf, V zero).
+        const bool bad0 = __builtin_amdgcn_readlane(pidU, KT == 0 ? 2 * blk : blk) < 0;
+        const bool bad1 = KT == 0 ? __builtin_amdgcn_readlane(pidU, 2 * blk + 1) < 0 : true;
+        if constexpr (KT == 0) {
+          if (tok0 + 32 > uEnd || bad0 || bad1) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-            if (t >= uEnd || ((e >> 2) ? bad1 : bad0)) {
-              if constexpr (D == 128)
-                r.v[e] = i32x2{0, 0};
-              else
-                r.v[e] = 0;
+            for (int e = 0; e < 8; ++e) {
+              const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+              if (t >= uEnd || ((e >> 2) ? bad1 : bad0)) {
+                if constexpr (D == 128)
+                  r.v[e] = i32x2{0, 0};
+                else
+                  r.v[e] = 0;
+              }
+            }
+          }
+        } else {
+          if (tok0 + 16 > uEnd || bad0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (tok0 + 4 * j + e >= uEnd || bad0) {
+                if constexpr (D == 128)
+                  r.v[e] = i32x4{0, 0, 0, 0};
+                else
+                  r.v[e] = i32x2{0, 0};
+              }
             }
           }
         }
@@ -664,19 +738,29 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
           sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
+        if constexpr (KT == 0) {
 #pragma unroll
-        for (int T = 0; T < 2; ++T) {
+          for (int T = 0; T < 2; ++T) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+              const i32x4 raw = r.k[T][s >> 1];
+              const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
+#pragma unroll
+              for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
+            }
+          }
+        } else {
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
-            const i32x4 raw = r.k[T][s >> 1];
-            const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
+            const qvec8 kop = __builtin_bit_cast(qvec8, r.k[s]);
 #pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
+            for (int qt = 0; qt < NQT; ++qt) sc[qt][0] = mfma16(kop, qop[qt][s], sc[qt][0]);
           }
         }
         // ---- online softmax (log2 domain) ----
-        const bool need_mask = (tok0 + 31 > min_lim) || bad0 || bad1;
-        f16x8 pop[NQT];
+        const bool need_mask = (tok0 + kTok - 1 > min_lim) || bad0 || bad1;
+        pvec8 pop[NQT];
+        pvec8 pop_lo[kSplitP ? NQT : 1];
 #pragma unroll
         for (int qt = 0; qt < NQT; ++qt) {
           float x[8];
@@ -708,50 +792,78 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           }
           const float m_use = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
           float psum = 0.0f;
-          i32x4 pw;
+          i32x4 pw, pw_lo;
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
             const float p0 = __builtin_amdgcn_exp2f(x[e] - m_use);
             const float p1 = __builtin_amdgcn_exp2f(x[e + 1] - m_use);
             psum += p0 + p1;
-            pw[e >> 1] = pack2<_Float16>(p0, p1);
+            pw[e >> 1] = pack2<PT>(p0, p1);
+            if constexpr (kSplitP) {
+              // bf16 -> f32 is exact: the halves are the top 16 bits of an f32
+              const uint32_t w = (uint32_t)pw[e >> 1];
+              pw_lo[e >> 1] = pack2<PT>(p0 - __builtin_bit_cast(float, w << 16),
+                                        p1 - __builtin_bit_cast(float, w & 0xffff0000u));
+            }
           }
-          pop[qt] = __builtin_bit_cast(f16x8, pw);
+          pop[qt] = __builtin_bit_cast(pvec8, pw);
+          if constexpr (kSplitP) pop_lo[qt] = __builtin_bit_cast(pvec8, pw_lo);
           l_run[qt] += psum;
         }
         // ---- O^T += V^T . P^T ----
+        // d tile t (0 <= t < D/16) holds dims 8*(lane%16) + t (D = 128) or
+        // 4*(lane%16) + t (D = 64); k slot i of the V^T and P^T operands is
+        // token 16*(i/4) + 4*(lane/16) + i%4 of the block.
 #pragma unroll
         for (int tp2 = 0; tp2 < NT; tp2 += 2) {
-          // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
           i32x4 wa, wb;
+          if constexpr (KT == 0) {
+            // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
 #pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            int w0, w1;
-            if constexpr (D == 128) {
-              w0 = r.v[e][tp2 >> 2];
-              w1 = r.v[e + 1][tp2 >> 2];
-            } else {
-              w0 = r.v[e];
-              w1 = r.v[e + 1];
+            for (int e = 0; e < 8; e += 2) {
+              int w0, w1;
+              if constexpr (D == 128) {
+                w0 = r.v[e][tp2 >> 2];
+                w1 = r.v[e + 1][tp2 >> 2];
+              } else {
+                w0 = r.v[e];
+                w1 = r.v[e + 1];
+              }
+              const f32x2 f0 = fp8x2_f32(w0, (tp2 & 3) != 0);
+              const f32x2 f1 = fp8x2_f32(w1, (tp2 & 3) != 0);
+              wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
+              wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
             }
-            const f32x2 f0 = fp8x2_f32(w0, (tp2 & 3) != 0);
-            const f32x2 f1 = fp8x2_f32(w1, (tp2 & 3) != 0);
-            wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
-            wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
+          } else {
+            // d tiles tp2, tp2+1 are the low and high halves of dword tp2 / 2:
+            // pair the halves of tokens (0, 1) and (2, 3); slots 4-7 are empty
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+              const uint32_t w0 = (uint32_t)r.v[e][tp2 >> 1];
+              const uint32_t w1 = (uint32_t)r.v[e + 1][tp2 >> 1];
+              wa[e >> 1] = (int)((w0 & 0xffffu) | (w1 << 16));
+              wb[e >> 1] = (int)((w0 >> 16) | (w1 & 0xffff0000u));
+            }
+            wa[2] = wa[3] = 0;
+            wb[2] = wb[3] = 0;
           }
-          const f16x8 va = __builtin_bit_cast(f16x8, wa);
-          const f16x8 vb = __builtin_bit_cast(f16x8, wb);
+          const pvec8 va = __builtin_bit_cast(pvec8, wa);
+          const pvec8 vb = __builtin_bit_cast(pvec8, wb);
 #pragma unroll
           for (int qt = 0; qt < NQT; ++qt) {
             acc[qt][tp2] = mfma16(va, pop[qt], acc[qt][tp2]);
             acc[qt][tp2 + 1] = mfma16(vb, pop[qt], acc[qt][tp2 + 1]);
+            if constexpr (kSplitP) {
+              acc[qt][tp2] = mfma16(va, pop_lo[qt], acc[qt][tp2]);
+              acc[qt][tp2 + 1] = mfma16(vb, pop_lo[qt], acc[qt][tp2 + 1]);
+            }
           }
         }
       };
 
       // Compute block k, then refill its buffer with stream position k + 2:
       // the unit's own block or, in order, the next unit's first two blocks.
-      auto step = [&](BlockRaw<D> &r, int k) {
+      auto step = [&](Block &r, int k) {
         compute_block(r, k);
         const int pos = k + 2;
         if (pos < nU) {
@@ -1087,6 +1199,12 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (!a) return fail(L20_PD_EINVAL, "null argument block");
   if (a->query_dtype != L20_PD_BF16 && a->query_dtype != L20_PD_FP16)
     return fail(L20_PD_EINVAL, "query must be bf16 or fp16");
+  if (a->kv_dtype != L20_PD_KV_FP8_E4M3 && a->kv_dtype != L20_PD_KV_FP16 && a->kv_dtype != L20_PD_KV_BF16)
+    return fail(L20_PD_EINVAL, "unknown K/V cache dtype");
+  const bool kv16 = a->kv_dtype != L20_PD_KV_FP8_E4M3;
+  if (kv16 && (a->kv_dtype == L20_PD_KV_BF16) != (a->query_dtype == L20_PD_BF16))
+    return fail(L20_PD_EINVAL, "query and 16-bit K/V cache must have the same dtype");
+  const int64_t es = kv16 ? 2 : 1;  // bytes per cache element
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(L20_PD_EINVAL, "NHD cache only: head_dim must be 64 or 128");
   if (a->page_size != 16) return fail(L20_PD_EINVAL, "NHD cache only: page_size must be 16");
@@ -1105,6 +1223,7 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (a->batch == 0) return L20_PD_OK;
   if (!a->query || !a->key_cache || !a->value_cache || !a->block_table || !a->seq_lens || !a->output)
     return fail(L20_PD_EINVAL, "null tensor pointer");
+  if (((uintptr_t)a->page_indptr % 4) != 0) return fail(L20_PD_EINVAL, "page_indptr must be int32-aligned");
   if (a->num_pages <= 0) return fail(L20_PD_EINVAL, "K/V cache has no pages");
   const int32_t n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
   if (n_s > 1) {
@@ -1117,19 +1236,19 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   for (int which = 0; which < 2; ++which) {
     const int64_t st = which ? a->v_stride_token : a->k_stride_token;
     const int64_t sh = which ? a->v_stride_head : a->k_stride_head;
-    if (st < 0 || sh < 0 || 15 * st + (int64_t)(a->num_kv_heads - 1) * sh + a->head_dim > INT32_MAX)
+    if (st < 0 || sh < 0 || (15 * st + (int64_t)(a->num_kv_heads - 1) * sh + a->head_dim) * es > INT32_MAX)
       return fail(L20_PD_EINVAL, "K/V token and head strides must be non-negative and span less than 2 GiB per page");
   }
-  if (a->bt_max_pages * (int64_t)16 < a->max_seq_len)
+  if (!a->page_indptr && a->bt_max_pages * (int64_t)16 < a->max_seq_len)
     return fail(L20_PD_EINVAL, "block table has fewer pages than max_seq_len needs");
-  // Vector-load alignment: 16 B K chunks, 8/4 B V chunks, 16 B query chunks.
-  const uint64_t kbits = (uint64_t)(uintptr_t)a->key_cache | (uint64_t)a->k_stride_page |
-                         (uint64_t)a->k_stride_token | (uint64_t)a->k_stride_head;
+  // Vector-load alignment: 16 B K chunks, V chunks of head_dim/16 elements, 16 B query chunks.
+  const uint64_t kbits = (uint64_t)(uintptr_t)a->key_cache | (uint64_t)(a->k_stride_page * es) |
+                         (uint64_t)(a->k_stride_token * es) | (uint64_t)(a->k_stride_head * es);
   if (kbits % 16 != 0) return fail(L20_PD_EINVAL, "K cache pointer and strides must be 16-byte aligned");
-  const uint64_t vbits = (uint64_t)(uintptr_t)a->value_cache | (uint64_t)a->v_stride_page |
-                         (uint64_t)a->v_stride_token | (uint64_t)a->v_stride_head;
-  if (vbits % (a->head_dim == 128 ? 8u : 4u) != 0)
-    return fail(L20_PD_EINVAL, "V cache pointer and strides must be aligned to head_dim/16 bytes");
+  const uint64_t vbits = (uint64_t)(uintptr_t)a->value_cache | (uint64_t)(a->v_stride_page * es) |
+                         (uint64_t)(a->v_stride_token * es) | (uint64_t)(a->v_stride_head * es);
+  if (vbits % (uint64_t)((a->head_dim / 16) * es) != 0)
+    return fail(L20_PD_EINVAL, "V cache pointer and strides must be aligned to head_dim/16 elements");
   if (((uintptr_t)a->query % 16) != 0 || (a->q_stride_row % 8) != 0 || (a->q_stride_head % 8) != 0)
     return fail(L20_PD_EINVAL, "query pointer and strides must be 16-byte aligned");
   if (((uintptr_t)a->output % 16) != 0 || (a->o_stride_row % 8) != 0 || (a->o_stride_head % 8) != 0)
@@ -1160,7 +1279,7 @@ bool partial_compact(int batch) { return batch <= l20pd::kMaxCompactBatch; }
 // at the kernel's occupancy, never more than there are split-major slots.
 // L20_PD_MAX_WORKGROUPS (a positive integer) caps the count, which lets tests
 // drive many items through each workgroup.
-template <typename QT, int D, int NQT>
+template <typename QT, int KT, int D, int NQT>
 int partial_grid(int threads, size_t lds, int64_t max_items) {
   static thread_local int cached_dev = -1, cached_threads = -1, cached_blocks = 0;
   static thread_local size_t cached_lds = 0;
@@ -1169,7 +1288,7 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
   if (dev != cached_dev || threads != cached_threads || lds != cached_lds) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, D, NQT>, threads, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, KT, D, NQT>, threads, lds) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
@@ -1186,16 +1305,26 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, max_items));
 }
 
-template <typename QT, int D, int NQT>
+template <typename QT, int KT, int D, int NQT>
 hipError_t launch_partial(l20pd::PartialParams pp, int batch, int num_kv_heads, hipStream_t stream) {
   const int nwaves = partial_waves(num_kv_heads);
   const int threads = 64 * nwaves;
   pp.compact = partial_compact(batch) ? 1 : 0;
   const size_t lds = pp.compact ? (size_t)(2 * batch + 1) * sizeof(int) : 0;
   const int64_t max_items = (int64_t)batch * pp.num_splits;
-  const int grid = partial_grid<QT, D, NQT>(threads, lds, max_items);
-  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, D, NQT>), dim3(grid), dim3(threads), lds, stream, pp);
+  const int grid = partial_grid<QT, KT, D, NQT>(threads, lds, max_items);
+  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, KT, D, NQT>), dim3(grid), dim3(threads), lds, stream, pp);
   return hipGetLastError();
+}
+
+template <typename QT, int KT>
+hipError_t launch_partial_shape(const l20pd::PartialParams &pp, int head_dim, int nqt, int batch, int num_kv_heads,
+                                hipStream_t stream) {
+  if (head_dim == 128)
+    return nqt == 1 ? launch_partial<QT, KT, 128, 1>(pp, batch, num_kv_heads, stream)
+                    : launch_partial<QT, KT, 128, 2>(pp, batch, num_kv_heads, stream);
+  return nqt == 1 ? launch_partial<QT, KT, 64, 1>(pp, batch, num_kv_heads, stream)
+                  : launch_partial<QT, KT, 64, 2>(pp, batch, num_kv_heads, stream);
 }
 
 template <typename QT, int D>
@@ -1205,23 +1334,34 @@ hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipSt
   return hipGetLastError();
 }
 
+// Tokens of a sequence the kernels may touch: the workspace's splits and,
+// with a block table, its row length (a CSR page list is bounded per
+// sequence inside the kernel).
+int length_cap(const l20_pd_fp8_args &a, int num_splits) {
+  const int64_t by_splits = (int64_t)num_splits * a.split_size;
+  if (a.page_indptr) return (int)by_splits;
+  return (int)std::min<int64_t>(by_splits, (int64_t)a.bt_max_pages * 16);
+}
+
 l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   l20pd::PartialParams pp;
   memset(&pp, 0, sizeof(pp));
   pp.q = a.query;
   pp.q_srow = a.q_stride_row;
   pp.q_shead = a.q_stride_head;
+  // The kernels address the caches in bytes.
+  const int64_t es = a.kv_dtype == L20_PD_KV_FP8_E4M3 ? 1 : 2;
   pp.k = a.key_cache;
-  pp.k_spage = a.k_stride_page;
-  pp.k_stok32 = (int)a.k_stride_token;
-  pp.k_shead32 = (int)a.k_stride_head;
+  pp.k_spage = a.k_stride_page * es;
+  pp.k_stok32 = (int)(a.k_stride_token * es);
+  pp.k_shead32 = (int)(a.k_stride_head * es);
   pp.v = a.value_cache;
-  pp.v_spage = a.v_stride_page;
-  pp.v_stok32 = (int)a.v_stride_token;
-  pp.v_shead32 = (int)a.v_stride_head;
+  pp.v_spage = a.v_stride_page * es;
+  pp.v_stok32 = (int)(a.v_stride_token * es);
+  pp.v_shead32 = (int)(a.v_stride_head * es);
   // Bytes one KV-head slice of a page can touch: the buffer range of its loads.
-  pp.k_extent = (int)(15 * a.k_stride_token + (int64_t)(a.num_kv_heads - 1) * a.k_stride_head + a.head_dim);
-  pp.v_extent = (int)(15 * a.v_stride_token + (int64_t)(a.num_kv_heads - 1) * a.v_stride_head + a.head_dim);
+  pp.k_extent = (int)((15 * a.k_stride_token + (int64_t)(a.num_kv_heads - 1) * a.k_stride_head + a.head_dim) * es);
+  pp.v_extent = (int)((15 * a.v_stride_token + (int64_t)(a.num_kv_heads - 1) * a.v_stride_head + a.head_dim) * es);
   pp.bt = a.block_table;
   pp.bt_srow = a.bt_stride_row;
   pp.seq_lens = a.seq_lens;
@@ -1257,10 +1397,10 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.split_size = a.split_size;
   pp.num_splits = n_s > 0 ? n_s : 1;
   pp.po_f32 = a.partial_dtype == L20_PD_FP32;
-  const int64_t cap = std::min<int64_t>((int64_t)pp.num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
-  pp.l_cap = (int)cap;
+  pp.l_cap = length_cap(a, pp.num_splits);
   pp.batch = a.batch;
   pp.bt_pages = a.bt_max_pages;
+  pp.indptr = a.page_indptr;
   return pp;
 }
 
@@ -1290,7 +1430,7 @@ l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
   mp.split_size = a.split_size;
   mp.num_splits = num_splits;
   mp.po_f32 = a.partial_dtype == L20_PD_FP32;
-  mp.l_cap = (int)std::min<int64_t>((int64_t)num_splits * a.split_size, (int64_t)a.bt_max_pages * 16);
+  mp.l_cap = length_cap(a, num_splits);
   mp.rows = a.batch * a.q_len;
   mp.num_q_heads = a.num_q_heads;
   return mp;
@@ -1299,10 +1439,17 @@ l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
 // Which kernels one call enqueues.
 enum Stage { kPartial = 1, kMerge = 2, kBoth = 3 };
 
-int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages) {
+// Which cache types an entry point accepts.
+enum KvKind { kKvFp8 = 1, kKv16 = 2, kKvAny = 3 };
+
+int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   g_last_error[0] = '\0';
   const int32_t rc = check_args(a);
   if (rc != L20_PD_OK) return rc;
+  const bool kv16 = a->kv_dtype != L20_PD_KV_FP8_E4M3;
+  if (!(kinds & (kv16 ? kKv16 : kKvFp8)))
+    return fail(L20_PD_EINVAL, kv16 ? "K/V cache must be torch.float8_e4m3fn"
+                                    : "K/V cache must be fp16 or bf16 for this entry point");
   if (a->batch == 0) return L20_PD_OK;
   const int n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
@@ -1314,21 +1461,13 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages) {
   const int rows = a->batch * a->q_len;
   hipError_t e = hipSuccess;
   if (stages & kPartial) {
-    if (a->head_dim == 128) {
-      if (nqt == 1)
-        e = bf16 ? launch_partial<__bf16, 128, 1>(pp, a->batch, a->num_kv_heads, stream)
-                 : launch_partial<_Float16, 128, 1>(pp, a->batch, a->num_kv_heads, stream);
-      else
-        e = bf16 ? launch_partial<__bf16, 128, 2>(pp, a->batch, a->num_kv_heads, stream)
-                 : launch_partial<_Float16, 128, 2>(pp, a->batch, a->num_kv_heads, stream);
-    } else {
-      if (nqt == 1)
-        e = bf16 ? launch_partial<__bf16, 64, 1>(pp, a->batch, a->num_kv_heads, stream)
-                 : launch_partial<_Float16, 64, 1>(pp, a->batch, a->num_kv_heads, stream);
-      else
-        e = bf16 ? launch_partial<__bf16, 64, 2>(pp, a->batch, a->num_kv_heads, stream)
-                 : launch_partial<_Float16, 64, 2>(pp, a->batch, a->num_kv_heads, stream);
-    }
+    const int D = a->head_dim, B = a->batch, H = a->num_kv_heads;
+    if (kv16)
+      e = bf16 ? launch_partial_shape<__bf16, 1>(pp, D, nqt, B, H, stream)
+               : launch_partial_shape<_Float16, 1>(pp, D, nqt, B, H, stream);
+    else
+      e = bf16 ? launch_partial_shape<__bf16, 0>(pp, D, nqt, B, H, stream)
+               : launch_partial_shape<_Float16, 0>(pp, D, nqt, B, H, stream);
   }
   // With a single split every row is finished by the partial kernel.
   if (e == hipSuccess && (stages & kMerge) && n_s > 1) {
@@ -1379,11 +1518,13 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
   return s;
 }
 
-int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth); }
+int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth, kKvFp8); }
 
-int32_t l20_pd_fp8_e4m3_partial(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kPartial); }
+int32_t l20_pd_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth, kKv16); }
 
-int32_t l20_pd_fp8_e4m3_merge(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kMerge); }
+int32_t l20_pd_fp8_e4m3_partial(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kPartial, kKvAny); }
+
+int32_t l20_pd_fp8_e4m3_merge(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kMerge, kKvAny); }
 
 int32_t l20_pd_fp8_e4m3_dequant_f32(const uint8_t *src, float *dst, int64_t n, float scale, void *stream) {
   g_last_error[0] = '\0';

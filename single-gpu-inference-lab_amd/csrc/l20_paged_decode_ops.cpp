@@ -1,6 +1,6 @@
-// TORCH_LIBRARY(l20_stack) binding of the MI355X paged FP8 decode op.
+// TORCH_LIBRARY(l20_stack) binding of the MI355X paged decode ops.
 //
-// Keeps the reference's schema for paged_decode_fp8_e4m3_split_out verbatim
+// paged_decode_fp8_e4m3_split_out keeps the reference's schema verbatim
 // (integrations/vllm/cuda/l20_paged_decode.cpp:128-135, relative to the
 // reference repo root) and appends defaulted arguments, so every 13-argument
 // legacy call still binds:
@@ -9,6 +9,11 @@
 //   Tensor? v_scale_per_head=None    (fp32 [Hkv]; overrides v_scale)
 //   int q_len=1                      (query rows [B*q_len, Hq, D], causal)
 //   Tensor(e!)? lse=None             (fp32 [B*q_len, Hq], natural log)
+// paged_decode_split_out (fp16/bf16 caches; schema :121-127) appends
+// softmax_scale, q_len and lse the same way; paged_decode_split_indices_out
+// is the CSR page-list variant the reference exports through pybind
+// (l20_paged_decode.cpp:150-152, l20_paged_decode.cu:600-649), registered
+// here with the same defaulted tail.
 // The implementation validates with the reference's TORCH_CHECK messages
 // (l20_paged_decode.cu:665-688) and calls the C ABI in
 // libl20_paged_decode_hip.so on the current HIP stream.  Nothing is
@@ -42,22 +47,24 @@ void check_same_device(const at::Tensor &t, const at::Tensor &query, const char 
   TORCH_CHECK(t.device() == query.device(), what, " must be on the query's device");
 }
 
-at::Tensor paged_decode_fp8_e4m3_split_out(
-    const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache,
-    const at::Tensor &block_table, const at::Tensor &seq_lens, const at::Tensor &partial_output,
-    const at::Tensor &partial_max, const at::Tensor &partial_sum, const at::Tensor &output, double k_scale,
-    double v_scale, int64_t max_seq_len, int64_t split_size, std::optional<double> softmax_scale,
-    const std::optional<at::Tensor> &k_scale_per_head, const std::optional<at::Tensor> &v_scale_per_head,
-    int64_t q_len, const std::optional<at::Tensor> &lse) {
-  TORCH_CHECK(query.is_cuda(), "query must be CUDA");
-  TORCH_CHECK(query.scalar_type() == at::kBFloat16 || query.scalar_type() == at::kHalf,
-              "query must be bf16 or fp16");
-  TORCH_CHECK(key_cache.scalar_type() == at::kFloat8_e4m3fn && value_cache.scalar_type() == at::kFloat8_e4m3fn,
-              "K/V cache must be torch.float8_e4m3fn");
+// Page addressing of one call: a [batch, max_pages] block table, or a CSR
+// page list (page_indptr [batch + 1], page_indices flat).
+struct PageTable {
+  const at::Tensor *table;
+  const at::Tensor *indptr;  // nullptr: block table
+};
+
+// Validation shared by the three ops and the argument block they pass to the
+// C ABI.  Cache-dtype checks are done by the callers.
+l20_pd_fp8_args make_args(const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache,
+                          const PageTable &pages, const at::Tensor &seq_lens, const at::Tensor &partial_output,
+                          const at::Tensor &partial_max, const at::Tensor &partial_sum, const at::Tensor &output,
+                          int64_t max_seq_len, int64_t split_size, std::optional<double> softmax_scale, int64_t q_len,
+                          const std::optional<at::Tensor> &lse, int32_t kv_dtype) {
   TORCH_CHECK(query.dim() == 3, "invalid query");
   TORCH_CHECK(key_cache.dim() == 4 && key_cache.size(3) == query.size(2), "NHD cache only");
   TORCH_CHECK(key_cache.sizes() == value_cache.sizes(), "K/V cache mismatch");
-  TORCH_CHECK(block_table.scalar_type() == at::kInt, "int32 block table");
+  TORCH_CHECK(pages.table->scalar_type() == at::kInt, pages.indptr ? "int32 page indices" : "int32 block table");
   TORCH_CHECK(seq_lens.scalar_type() == at::kInt, "int32 sequence lengths");
   TORCH_CHECK(q_len >= 1, "q_len must be >= 1");
   TORCH_CHECK(query.size(1) % key_cache.size(2) == 0, "Q heads must be divisible by KV heads");
@@ -66,12 +73,21 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
   const int64_t batch = rows / q_len;
   const int64_t heads = query.size(1);
   const int64_t head_dim = query.size(2);
-  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == batch, "block table must be [batch, max_pages]");
+  if (pages.indptr) {
+    const at::Tensor &ip = *pages.indptr;
+    TORCH_CHECK(ip.scalar_type() == at::kInt && ip.dim() == 1 && ip.size(0) == batch + 1 && ip.is_contiguous(),
+                "page_indptr must be contiguous int32 [batch + 1]");
+    TORCH_CHECK(pages.table->dim() == 1 && pages.table->is_contiguous(), "page_indices must be contiguous 1-D");
+    check_same_device(ip, query, "page_indptr");
+  } else {
+    TORCH_CHECK(pages.table->dim() == 2 && pages.table->size(0) == batch, "block table must be [batch, max_pages]");
+    TORCH_CHECK(pages.table->stride(1) == 1, "block table rows and seq_lens must be contiguous");
+  }
   TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.size(0) == batch, "seq_lens must be [batch]");
-  TORCH_CHECK(block_table.stride(1) == 1 && seq_lens.is_contiguous(), "block table rows and seq_lens must be contiguous");
+  TORCH_CHECK(seq_lens.is_contiguous(), "block table rows and seq_lens must be contiguous");
   TORCH_CHECK(output.sizes() == query.sizes() && output.scalar_type() == query.scalar_type(),
               "output must match the query's shape and dtype");
-  for (const at::Tensor *t : {&key_cache, &value_cache, &block_table, &seq_lens, &output})
+  for (const at::Tensor *t : {&key_cache, &value_cache, pages.table, &seq_lens, &output})
     check_same_device(*t, query, "every tensor");
   TORCH_CHECK(query.stride(2) == 1 && key_cache.stride(3) == 1 && value_cache.stride(3) == 1 &&
                   output.stride(2) == 1,
@@ -92,17 +108,6 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
       check_same_device(*t, query, "partial max/sum workspace");
     }
     check_same_device(partial_output, query, "partial output workspace");
-  }
-  const float *ksph = nullptr, *vsph = nullptr;
-  for (int which = 0; which < 2; ++which) {
-    const auto &opt = which == 0 ? k_scale_per_head : v_scale_per_head;
-    if (opt.has_value() && opt->defined()) {
-      const at::Tensor &t = *opt;
-      TORCH_CHECK(t.scalar_type() == at::kFloat && t.is_contiguous() && t.numel() == key_cache.size(2),
-                  "per-head scales must be contiguous fp32 [num_kv_heads]");
-      check_same_device(t, query, "per-head scales");
-      (which == 0 ? ksph : vsph) = t.data_ptr<float>();
-    }
   }
   float *lse_ptr = nullptr;
   int64_t lse_srow = 0, lse_shead = 0;
@@ -131,9 +136,13 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
   a.v_stride_head = value_cache.stride(2);
   a.num_pages = key_cache.size(0);
   a.page_size = (int32_t)key_cache.size(1);
-  a.block_table = block_table.data_ptr<int32_t>();
-  a.bt_stride_row = block_table.stride(0);
-  a.bt_max_pages = (int32_t)block_table.size(1);
+  a.block_table = pages.table->data_ptr<int32_t>();
+  if (pages.indptr) {
+    a.page_indptr = pages.indptr->data_ptr<int32_t>();
+  } else {
+    a.bt_stride_row = pages.table->stride(0);
+    a.bt_max_pages = (int32_t)pages.table->size(1);
+  }
   a.seq_lens = seq_lens.data_ptr<int32_t>();
   if (need_ws) {
     a.partial_output = partial_output.data_ptr();
@@ -157,10 +166,8 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
   a.lse = lse_ptr;
   a.lse_stride_row = lse_srow;
   a.lse_stride_head = lse_shead;
-  a.k_scale = (float)k_scale;
-  a.v_scale = (float)v_scale;
-  a.k_scale_per_head = ksph;
-  a.v_scale_per_head = vsph;
+  a.k_scale = 1.0f;
+  a.v_scale = 1.0f;
   a.softmax_scale = softmax_scale.has_value() ? (float)*softmax_scale : 0.0f;
   a.batch = (int32_t)batch;
   a.q_len = (int32_t)q_len;
@@ -169,17 +176,106 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
   a.head_dim = (int32_t)head_dim;
   a.max_seq_len = (int32_t)max_seq_len;
   a.split_size = (int32_t)split_size;
+  a.kv_dtype = kv_dtype;
+  return a;
+}
 
+void launch(const at::Tensor &query, const l20_pd_fp8_args &a, bool fp8) {
   const c10::DeviceGuard guard(query.device());
   void *stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.get_device()).stream();
-  const int32_t rc = l20_pd_fp8_e4m3_split_out(&a, stream);
+  const int32_t rc = fp8 ? l20_pd_fp8_e4m3_split_out(&a, stream) : l20_pd_split_out(&a, stream);
   TORCH_CHECK(rc == L20_PD_OK, l20_pd_last_error());
+}
+
+void check_query(const at::Tensor &query) {
+  TORCH_CHECK(query.is_cuda(), "query must be CUDA");
+  TORCH_CHECK(query.scalar_type() == at::kBFloat16 || query.scalar_type() == at::kHalf,
+              "query must be bf16 or fp16");
+}
+
+// 16-bit caches: the reference's fp16 op (FP16 only there); bf16 caches pair
+// with a bf16 query.
+int32_t check_16bit_cache(const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache) {
+  TORCH_CHECK(key_cache.scalar_type() == query.scalar_type() && value_cache.scalar_type() == query.scalar_type(),
+              "K/V cache must have the query's dtype (fp16 or bf16)");
+  return query.scalar_type() == at::kBFloat16 ? L20_PD_KV_BF16 : L20_PD_KV_FP16;
+}
+
+at::Tensor paged_decode_fp8_e4m3_split_out(
+    const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache,
+    const at::Tensor &block_table, const at::Tensor &seq_lens, const at::Tensor &partial_output,
+    const at::Tensor &partial_max, const at::Tensor &partial_sum, const at::Tensor &output, double k_scale,
+    double v_scale, int64_t max_seq_len, int64_t split_size, std::optional<double> softmax_scale,
+    const std::optional<at::Tensor> &k_scale_per_head, const std::optional<at::Tensor> &v_scale_per_head,
+    int64_t q_len, const std::optional<at::Tensor> &lse) {
+  check_query(query);
+  TORCH_CHECK(key_cache.scalar_type() == at::kFloat8_e4m3fn && value_cache.scalar_type() == at::kFloat8_e4m3fn,
+              "K/V cache must be torch.float8_e4m3fn");
+  l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&block_table, nullptr}, seq_lens,
+                                partial_output, partial_max, partial_sum, output, max_seq_len, split_size,
+                                softmax_scale, q_len, lse, L20_PD_KV_FP8_E4M3);
+  for (int which = 0; which < 2; ++which) {
+    const auto &opt = which == 0 ? k_scale_per_head : v_scale_per_head;
+    if (opt.has_value() && opt->defined()) {
+      const at::Tensor &t = *opt;
+      TORCH_CHECK(t.scalar_type() == at::kFloat && t.is_contiguous() && t.numel() == key_cache.size(2),
+                  "per-head scales must be contiguous fp32 [num_kv_heads]");
+      check_same_device(t, query, "per-head scales");
+      (which == 0 ? a.k_scale_per_head : a.v_scale_per_head) = t.data_ptr<float>();
+    }
+  }
+  a.k_scale = (float)k_scale;
+  a.v_scale = (float)v_scale;
+  launch(query, a, true);
+  return output;
+}
+
+// l20_paged_decode_split_out_cuda (l20_paged_decode.cu:549-597).
+at::Tensor paged_decode_split_out(const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache,
+                                  const at::Tensor &block_table, const at::Tensor &seq_lens,
+                                  const at::Tensor &partial_output, const at::Tensor &partial_max,
+                                  const at::Tensor &partial_sum, const at::Tensor &output, int64_t max_seq_len,
+                                  int64_t split_size, std::optional<double> softmax_scale, int64_t q_len,
+                                  const std::optional<at::Tensor> &lse) {
+  check_query(query);
+  const int32_t kv = check_16bit_cache(query, key_cache, value_cache);
+  const l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&block_table, nullptr}, seq_lens,
+                                      partial_output, partial_max, partial_sum, output, max_seq_len, split_size,
+                                      softmax_scale, q_len, lse, kv);
+  launch(query, a, false);
+  return output;
+}
+
+// l20_paged_decode_split_indices_out_cuda (l20_paged_decode.cu:600-649): CSR page list.
+at::Tensor paged_decode_split_indices_out(const at::Tensor &query, const at::Tensor &key_cache,
+                                          const at::Tensor &value_cache, const at::Tensor &page_indptr,
+                                          const at::Tensor &page_indices, const at::Tensor &seq_lens,
+                                          const at::Tensor &partial_output, const at::Tensor &partial_max,
+                                          const at::Tensor &partial_sum, const at::Tensor &output,
+                                          int64_t max_seq_len, int64_t split_size,
+                                          std::optional<double> softmax_scale, int64_t q_len,
+                                          const std::optional<at::Tensor> &lse) {
+  check_query(query);
+  const int32_t kv = check_16bit_cache(query, key_cache, value_cache);
+  const l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&page_indices, &page_indptr},
+                                      seq_lens, partial_output, partial_max, partial_sum, output, max_seq_len,
+                                      split_size, softmax_scale, q_len, lse, kv);
+  launch(query, a, false);
   return output;
 }
 
 }  // namespace
 
 TORCH_LIBRARY(l20_stack, m) {
+  m.def(
+      "paged_decode_split_out("
+      "Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, Tensor seq_lens, "
+      "Tensor(a!) partial_output, Tensor(b!) partial_max, "
+      "Tensor(c!) partial_sum, Tensor(d!) output, "
+      "int max_seq_len, int split_size, "
+      "float? softmax_scale=None, int q_len=1, "
+      "Tensor(e!)? lse=None) -> Tensor(d!)");
   m.def(
       "paged_decode_fp8_e4m3_split_out("
       "Tensor query, Tensor key_cache, Tensor value_cache, "
@@ -191,8 +287,19 @@ TORCH_LIBRARY(l20_stack, m) {
       "float? softmax_scale=None, Tensor? k_scale_per_head=None, "
       "Tensor? v_scale_per_head=None, int q_len=1, "
       "Tensor(e!)? lse=None) -> Tensor(d!)");
+  m.def(
+      "paged_decode_split_indices_out("
+      "Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor page_indptr, Tensor page_indices, Tensor seq_lens, "
+      "Tensor(a!) partial_output, Tensor(b!) partial_max, "
+      "Tensor(c!) partial_sum, Tensor(d!) output, "
+      "int max_seq_len, int split_size, "
+      "float? softmax_scale=None, int q_len=1, "
+      "Tensor(e!)? lse=None) -> Tensor(d!)");
 }
 
 TORCH_LIBRARY_IMPL(l20_stack, CUDA, m) {
+  m.impl("paged_decode_split_out", &paged_decode_split_out);
   m.impl("paged_decode_fp8_e4m3_split_out", &paged_decode_fp8_e4m3_split_out);
+  m.impl("paged_decode_split_indices_out", &paged_decode_split_indices_out);
 }

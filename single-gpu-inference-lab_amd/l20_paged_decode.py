@@ -1,11 +1,13 @@
-"""Dispatcher-backed entry point for the MI355X paged FP8 decode operator.
+"""Dispatcher-backed entry points for the MI355X paged decode operators.
 
 Mirrors ``integrations/vllm/l20_paged_decode.py:1-117`` of the reference
 (paths relative to its repo root): ``load_library()`` loads
-``l20_paged_decode_ops.so`` from beside this file, ``paged_decode_fp8_e4m3_split_out``
-calls ``torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out`` and a
-``register_fake`` meta implementation returns ``output`` so the op traces
-under FakeTensor / torch.compile.  Both run at import.
+``l20_paged_decode_ops.so`` from beside this file; ``paged_decode_split_out``
+(fp16/bf16 caches), ``paged_decode_fp8_e4m3_split_out`` (fp8 caches) and
+``paged_decode_split_indices_out`` (16-bit caches, CSR page lists) call the
+``torch.ops.l20_stack`` ops of the same names, and ``register_fake`` meta
+implementations return ``output`` so the ops trace under FakeTensor /
+torch.compile.  Both run at import.
 
 The native library is required: importing this module raises if the built
 ``.so`` is missing, and the op has no CPU implementation to fall back on.
@@ -38,6 +40,58 @@ def load_library(path: Optional[Union[str, Path]] = None) -> None:
         return
     torch.ops.load_library(str(library))
     _loaded = True
+
+
+def paged_decode_split_out(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    partial_output: torch.Tensor,
+    partial_max: torch.Tensor,
+    partial_sum: torch.Tensor,
+    output: torch.Tensor,
+    max_seq_len: int,
+    split_size: int,
+    softmax_scale: Optional[float] = None,
+    q_len: int = 1,
+    lse: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Paged split-KV decode attention over fp16 (or bf16) caches; writes and
+    returns ``output``.  The first 11 arguments are the reference's
+    (``l20_paged_decode.py:20-45``)."""
+    return torch.ops.l20_stack.paged_decode_split_out(
+        query, key_cache, value_cache, block_table, seq_lens, partial_output, partial_max, partial_sum,
+        output, int(max_seq_len), int(split_size), None if softmax_scale is None else float(softmax_scale),
+        int(q_len), lse,
+    )
+
+
+def paged_decode_split_indices_out(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    page_indptr: torch.Tensor,
+    page_indices: torch.Tensor,
+    seq_lens: torch.Tensor,
+    partial_output: torch.Tensor,
+    partial_max: torch.Tensor,
+    partial_sum: torch.Tensor,
+    output: torch.Tensor,
+    max_seq_len: int,
+    split_size: int,
+    softmax_scale: Optional[float] = None,
+    q_len: int = 1,
+    lse: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """The CSR page-list variant (``l20_paged_decode.cu:600-649``): sequence b's
+    pages are ``page_indices[page_indptr[b] : page_indptr[b + 1]]``."""
+    return torch.ops.l20_stack.paged_decode_split_indices_out(
+        query, key_cache, value_cache, page_indptr, page_indices, seq_lens, partial_output, partial_max,
+        partial_sum, output, int(max_seq_len), int(split_size),
+        None if softmax_scale is None else float(softmax_scale), int(q_len), lse,
+    )
 
 
 def paged_decode_fp8_e4m3_split_out(
@@ -88,6 +142,18 @@ def paged_decode_fp8_e4m3_split_out(
 
 
 def _register_fake() -> None:
+    @torch.library.register_fake("l20_stack::paged_decode_split_out")
+    def _paged_decode_split_out_fake(query, key_cache, value_cache, block_table, seq_lens, partial_output,
+                                     partial_max, partial_sum, output, max_seq_len, split_size,
+                                     softmax_scale=None, q_len=1, lse=None):
+        return output
+
+    @torch.library.register_fake("l20_stack::paged_decode_split_indices_out")
+    def _paged_decode_split_indices_out_fake(query, key_cache, value_cache, page_indptr, page_indices, seq_lens,
+                                             partial_output, partial_max, partial_sum, output, max_seq_len,
+                                             split_size, softmax_scale=None, q_len=1, lse=None):
+        return output
+
     @torch.library.register_fake("l20_stack::paged_decode_fp8_e4m3_split_out")
     def _paged_decode_fp8_e4m3_split_out_fake(
         query,

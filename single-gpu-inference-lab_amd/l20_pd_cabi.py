@@ -16,6 +16,8 @@ LIB_PATH = Path(__file__).with_name("libl20_paged_decode_hip.so")
 
 L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
 L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
+L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16 = 0, 1, 2
+ABI_VERSION = 2
 
 # Every extern "C" symbol declared in include/l20_paged_decode.h.
 EXPORTED = (
@@ -24,6 +26,7 @@ EXPORTED = (
     "l20_pd_num_splits",
     "l20_pd_fp8_e4m3_check",
     "l20_pd_fp8_e4m3_split_out",
+    "l20_pd_split_out",
     "l20_pd_fp8_e4m3_partial",
     "l20_pd_fp8_e4m3_merge",
     "l20_pd_default_split_size",
@@ -56,6 +59,7 @@ class L20PdFp8Args(ctypes.Structure):
         ("softmax_scale", _f32),
         ("batch", _i32), ("q_len", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
         ("max_seq_len", _i32), ("split_size", _i32),
+        ("kv_dtype", _i32), ("page_indptr", _vp),
     ]
 
 
@@ -78,7 +82,8 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     args_p = ctypes.POINTER(L20PdFp8Args)
     lib.l20_pd_fp8_e4m3_check.argtypes = [args_p]
     lib.l20_pd_fp8_e4m3_check.restype = _i32
-    for name in ("l20_pd_fp8_e4m3_split_out", "l20_pd_fp8_e4m3_partial", "l20_pd_fp8_e4m3_merge"):
+    for name in ("l20_pd_fp8_e4m3_split_out", "l20_pd_split_out", "l20_pd_fp8_e4m3_partial",
+                 "l20_pd_fp8_e4m3_merge"):
         getattr(lib, name).argtypes = [args_p, _vp]
         getattr(lib, name).restype = _i32
     lib.l20_pd_default_split_size.argtypes = [_i32, _i32, _i32, _i32]
@@ -106,11 +111,26 @@ def _dtype_code(t) -> int:
     return {torch.bfloat16: L20_PD_BF16, torch.float16: L20_PD_FP16, torch.float32: L20_PD_FP32}[t.dtype]
 
 
+def _kv_code(t) -> int:
+    import torch
+
+    if t.dtype == torch.float16:
+        return L20_PD_KV_FP16
+    if t.dtype == torch.bfloat16:
+        return L20_PD_KV_BF16
+    return L20_PD_KV_FP8_E4M3
+
+
 def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, partial_output, partial_max,
                       partial_sum, output, k_scale, v_scale, max_seq_len, split_size, *, softmax_scale=None,
-                      k_scale_per_head=None, v_scale_per_head=None, q_len=1, lse=None) -> L20PdFp8Args:
-    """Fill ``l20_pd_fp8_args`` from tensors (same argument order as the op)."""
+                      k_scale_per_head=None, v_scale_per_head=None, q_len=1, lse=None,
+                      page_indptr=None) -> L20PdFp8Args:
+    """Fill ``l20_pd_fp8_args`` from tensors (same argument order as the fp8 op).
+
+    The cache dtype picks ``kv_dtype`` (fp8 e4m3fn, fp16 or bf16).  With
+    ``page_indptr`` [B+1], ``block_table`` is the flat CSR page list."""
     a = L20PdFp8Args()
+    a.kv_dtype = _kv_code(key_cache)
     a.query = query.data_ptr()
     a.query_dtype = _dtype_code(query)
     a.q_stride_row, a.q_stride_head = query.stride(0), query.stride(1)
@@ -120,7 +140,10 @@ def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, part
     a.v_stride_page, a.v_stride_token, a.v_stride_head = value_cache.stride()[:3]
     a.num_pages, a.page_size = key_cache.shape[0], key_cache.shape[1]
     a.block_table = block_table.data_ptr()
-    a.bt_stride_row, a.bt_max_pages = block_table.stride(0), block_table.shape[1]
+    if page_indptr is not None:
+        a.page_indptr = page_indptr.data_ptr()
+    else:
+        a.bt_stride_row, a.bt_max_pages = block_table.stride(0), block_table.shape[1]
     a.seq_lens = seq_lens.data_ptr()
     if partial_output is not None:
         a.partial_output = partial_output.data_ptr()
@@ -158,8 +181,10 @@ def _call(name: str, args: L20PdFp8Args, stream: int, lib: Optional[ctypes.CDLL]
 
 
 def split_out(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
-    """Call ``l20_pd_fp8_e4m3_split_out``; raise RuntimeError with the library's message on failure."""
-    _call("l20_pd_fp8_e4m3_split_out", args, stream, lib)
+    """Call ``l20_pd_fp8_e4m3_split_out`` (fp8 caches) or ``l20_pd_split_out`` (16-bit
+    caches); raise RuntimeError with the library's message on failure."""
+    name = "l20_pd_fp8_e4m3_split_out" if args.kv_dtype == L20_PD_KV_FP8_E4M3 else "l20_pd_split_out"
+    _call(name, args, stream, lib)
 
 
 def partial(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:

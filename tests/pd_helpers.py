@@ -157,3 +157,85 @@ def compare(out, lse, exp_out, exp_lse, rows: Optional[np.ndarray] = None, check
         res["lse_rel"] = float(err.max()) if err.size else 0.0
         assert res["lse_rel"] <= LSE_RTOL, res
     return res
+
+
+# ------------------------------------------------------------ 16-bit caches, CSR page lists
+def make_synthetic16(batch, hq, hkv, d, lens, *, dtype=torch.float16, q_len=1, seed=0, device="cuda",
+                     pool_extra=7, garbage_tail=False, csr_pad=0):
+    """Seeded inputs for the fp16/bf16-KV siblings: query and caches of ``dtype``, a
+    block table and the same pages as a CSR list (``csr_pad`` garbage entries after
+    each row, so that offsets and not row lengths are exercised)."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.as_tensor(lens, dtype=torch.int32)
+    pages_per = (lens.to(torch.int64) + 15) // 16
+    pool = int(pages_per.sum()) + pool_extra
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    mp = max(1, int(pages_per.max()))
+    table = torch.full((batch, mp), -7, dtype=torch.int32)
+    indices, indptr = [], [0]
+    off = 0
+    for b in range(batch):
+        n = int(pages_per[b])
+        table[b, :n] = perm[off:off + n]
+        indices.append(perm[off:off + n])
+        if csr_pad:
+            indices.append(torch.full((csr_pad,), 10**6, dtype=torch.int32))
+        indptr.append(indptr[-1] + n + csr_pad)
+        off += n
+    query = torch.randn(batch * q_len, hq, d, generator=g).to(dtype)
+    kc = torch.randn(pool, 16, hkv, d, generator=g).to(dtype)
+    vc = torch.randn(pool, 16, hkv, d, generator=g).to(dtype)
+    if garbage_tail:
+        for c in (kc, vc):
+            for b in range(batch):
+                L = int(lens[b])
+                if L % 16:
+                    c[int(table[b, L // 16]), L % 16:] = float("nan")
+    return {
+        "query": query.to(device), "key_cache": kc.to(device), "value_cache": vc.to(device),
+        "block_table": table.to(device), "seq_lens": lens.to(device),
+        "page_indices": (torch.cat(indices) if indices else torch.zeros(0, dtype=torch.int32)).to(device),
+        "page_indptr": torch.tensor(indptr, dtype=torch.int32).to(device),
+        "softmax_scale": None, "q_len": q_len, "max_seq_len": int(lens.max()) if len(lens) else 0,
+    }
+
+
+def run_op16(inp, split_size, *, via="torch", csr=False, partial_dtype=torch.float32, with_lse=True):
+    """Run the 16-bit-cache sibling (block table or CSR); returns ``(out, lse)``."""
+    import l20_paged_decode  # noqa: F401
+    import l20_pd_cabi as cabi
+
+    q = inp["query"]
+    po, pm, ps = workspace(inp, split_size, partial_dtype)
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device) if with_lse else None
+    if via == "torch":
+        if csr:
+            torch.ops.l20_stack.paged_decode_split_indices_out(
+                q, inp["key_cache"], inp["value_cache"], inp["page_indptr"], inp["page_indices"], inp["seq_lens"],
+                po, pm, ps, out, inp["max_seq_len"], split_size, inp["softmax_scale"], inp["q_len"], lse)
+        else:
+            torch.ops.l20_stack.paged_decode_split_out(
+                q, inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"], po, pm, ps, out,
+                inp["max_seq_len"], split_size, inp["softmax_scale"], inp["q_len"], lse)
+    else:
+        table = inp["page_indices"] if csr else inp["block_table"]
+        args = cabi.args_from_tensors(
+            q, inp["key_cache"], inp["value_cache"], table, inp["seq_lens"], po, pm, ps, out, 1.0, 1.0,
+            inp["max_seq_len"], split_size, softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], lse=lse,
+            page_indptr=inp["page_indptr"] if csr else None)
+        cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def run_oracle16(inp, rows: Optional[Sequence[int]] = None, csr=False):
+    """The CPU oracle for 16-bit caches on the same values; numpy ``(out, lse)``."""
+    from oracle import paged_fp8_decode_ref as ref
+
+    table = inp["page_indices"] if csr else inp["block_table"]
+    return ref.reference_dense_kv(
+        inp["query"].float().cpu().numpy(), inp["key_cache"].float().cpu().numpy(),
+        inp["value_cache"].float().cpu().numpy(), table.cpu().numpy(), inp["seq_lens"].cpu().numpy(),
+        softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows,
+        page_indptr=inp["page_indptr"].cpu().numpy() if csr else None)

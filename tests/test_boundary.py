@@ -37,7 +37,7 @@ def test_library_exports_every_header_symbol():
     assert sorted(cabi.EXPORTED) == declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.l20_pd_abi_version() == 1
+    assert lib.l20_pd_abi_version() == cabi.ABI_VERSION == 2
 
 
 def test_num_splits_and_default_split_size():
@@ -220,3 +220,71 @@ def test_kernel_source_contracts():
                    "K/V cache must be torch.float8_e4m3fn", "int32 block table", "int32 sequence lengths"):
         assert needle in ops, needle
     assert "hipMalloc" not in src and "hipMemset" not in src  # the op allocates nothing
+
+
+# ------------------------------------------------------------------ fp16/bf16-KV siblings, CSR
+# integrations/vllm/cuda/l20_paged_decode.cpp:121-127 (reference schema, kept verbatim)
+REFERENCE_FP16_SCHEMA_PREFIX = (
+    "l20_stack::paged_decode_split_out(Tensor query, Tensor key_cache, Tensor value_cache, "
+    "Tensor block_table, Tensor seq_lens, Tensor(a!) partial_output, Tensor(b!) partial_max, "
+    "Tensor(c!) partial_sum, Tensor(d!) output, int max_seq_len, int split_size"
+)
+
+
+def test_sibling_ops_keep_reference_schema_and_extend_it():
+    import l20_paged_decode  # noqa: F401
+
+    schema = str(torch.ops.l20_stack.paged_decode_split_out.default._schema)
+    assert schema.startswith(REFERENCE_FP16_SCHEMA_PREFIX)
+    for extra in ("float? softmax_scale=None", "int q_len=1", "Tensor(e!)? lse=None"):
+        assert extra in schema
+    csr = str(torch.ops.l20_stack.paged_decode_split_indices_out.default._schema)
+    # argument order of l20_paged_decode_split_indices_out_cuda (l20_paged_decode.cu:600-612)
+    assert csr.startswith(
+        "l20_stack::paged_decode_split_indices_out(Tensor query, Tensor key_cache, Tensor value_cache, "
+        "Tensor page_indptr, Tensor page_indices, Tensor seq_lens, Tensor(a!) partial_output, "
+        "Tensor(b!) partial_max, Tensor(c!) partial_sum, Tensor(d!) output, int max_seq_len, int split_size")
+
+
+def test_sibling_fakes_return_output_alias():
+    import l20_paged_decode
+
+    q, kc, vc, bt, sl, po, pm, ps, out = _meta_inputs()
+    kc16 = torch.empty(kc.shape, dtype=torch.bfloat16, device="meta")
+    r = l20_paged_decode.paged_decode_split_out(q, kc16, kc16, bt, sl, po, pm, ps, out, 128, 64)
+    assert r.shape == out.shape and r.device.type == "meta"
+    ip = torch.empty(q.shape[0] + 1, dtype=torch.int32, device="meta")
+    idx = torch.empty(64, dtype=torch.int32, device="meta")
+    r = l20_paged_decode.paged_decode_split_indices_out(q, kc16, kc16, ip, idx, sl, po, pm, ps, out, 128, 64)
+    assert r.shape == out.shape
+
+
+def test_check_16bit_caches_and_csr():
+    lib = cabi.load()
+    a = valid_args()
+    a.kv_dtype = cabi.L20_PD_KV_BF16  # bf16 query, strides now in elements
+    cabi.check(a)
+    a.query_dtype = cabi.L20_PD_FP16
+    with pytest.raises(RuntimeError, match="query and 16-bit K/V cache must have the same dtype"):
+        cabi.check(a)
+    a = valid_args()
+    a.kv_dtype = 7
+    with pytest.raises(RuntimeError, match="unknown K/V cache dtype"):
+        cabi.check(a)
+    # entry points accept only their cache types
+    a = valid_args()
+    assert lib.l20_pd_split_out(ctypes.byref(a), None) == cabi.L20_PD_EINVAL
+    assert "fp16 or bf16" in cabi.last_error(lib)
+    a.kv_dtype = cabi.L20_PD_KV_BF16
+    assert lib.l20_pd_fp8_e4m3_split_out(ctypes.byref(a), None) == cabi.L20_PD_EINVAL
+    assert "float8_e4m3fn" in cabi.last_error(lib)
+    # a CSR page list needs no block-table row length
+    a = valid_args()
+    a.page_indptr, a.bt_max_pages = 0x10000, 0
+    cabi.check(a)
+    # 16-bit V rows need head_dim/16-element alignment (8 elements = 16 B at D=128)
+    a = valid_args()
+    a.kv_dtype = cabi.L20_PD_KV_BF16
+    a.v_stride_head = 132
+    with pytest.raises(RuntimeError, match="V cache pointer and strides must be aligned"):
+        cabi.check(a)

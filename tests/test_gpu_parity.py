@@ -239,3 +239,63 @@ def test_work_queue_small_grids(case, max_wg, monkeypatch):
     exp = H.run_oracle(inp)
     for _ in range(2):  # the queue counters reset themselves between launches
         H.compare(*H.run_op(inp, split), *exp)
+
+
+# ------------------------------------------------------------ fp16/bf16-KV siblings (block table and CSR)
+# The reference benchmark's shapes (benchmark_cuda_paged_decode.py:63-101): batch 1/4,
+# contexts 512/2048/4096, fp16, 128-dim heads.
+SIB_REF = [(1, 512), (4, 2048), (4, 4096)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("batch,ctx", SIB_REF)
+@pytest.mark.parametrize("csr", [False, True], ids=["table", "csr"])
+def test_16bit_kv_reference_shapes(dtype, batch, ctx, csr):
+    inp = H.make_synthetic16(batch, 32, 8, 128, [ctx] * batch, dtype=dtype, seed=ctx + batch, csr_pad=2)
+    exp = H.run_oracle16(inp, csr=csr)
+    H.compare(*H.run_op16(inp, 512, csr=csr), *exp)
+
+
+SIB_EDGE = [
+    # name, batch, hq, hkv, d, lens, q_len
+    ("ragged_d128", 5, 28, 4, 128, [1, 15, 16, 33, 1025], 1),
+    ("ragged_d64", 4, 14, 2, 64, [0, 40, 511, 17], 1),
+    ("mha", 2, 4, 4, 128, [200, 90], 1),
+    ("group16_verify_q2", 2, 32, 2, 128, [65, 300], 2),
+    ("verify_q4", 3, 16, 2, 128, [70, 4, 513], 4),
+]
+
+
+@pytest.mark.parametrize("case", SIB_EDGE, ids=[c[0] for c in SIB_EDGE])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("split", [64, 1024])
+def test_16bit_kv_edge_cases(case, dtype, split):
+    name, batch, hq, hkv, d, lens, q_len = case
+    inp = H.make_synthetic16(batch, hq, hkv, d, lens, dtype=dtype, q_len=q_len, garbage_tail=True,
+                             seed=zlib.crc32(name.encode()) % 1000, csr_pad=1)
+    exp = H.run_oracle16(inp)
+    H.compare(*H.run_op16(inp, split), *exp)
+    H.compare(*H.run_op16(inp, split, csr=True, via="cabi"), *exp)
+
+
+def test_16bit_kv_fp16_partials_and_small_grid(monkeypatch):
+    monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", "3")
+    inp = H.make_synthetic16(6, 16, 2, 128, [3000, 0, 17, 700, 64, 1], dtype=torch.float16, seed=44)
+    exp = H.run_oracle16(inp)
+    for _ in range(2):
+        H.compare(*H.run_op16(inp, 64, partial_dtype=torch.float16), *exp)
+
+
+def test_fp8_op_rejects_16bit_caches_and_vice_versa():
+    inp = H.make_synthetic16(2, 8, 2, 128, [40, 20], dtype=torch.float16, seed=1)
+    po, pm, ps = H.workspace(inp, 64)
+    out = torch.empty_like(inp["query"])
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
+            inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"], po, pm, ps, out,
+            1.0, 1.0, inp["max_seq_len"], 64)
+    fp8 = H.make_synthetic(2, 8, 2, 128, [40, 20], seed=1)
+    with pytest.raises(RuntimeError, match="query's dtype"):
+        torch.ops.l20_stack.paged_decode_split_out(
+            fp8["query"], fp8["key_cache"], fp8["value_cache"], fp8["block_table"], fp8["seq_lens"], po, pm, ps,
+            torch.empty_like(fp8["query"]), fp8["max_seq_len"], 64)

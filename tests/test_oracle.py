@@ -285,3 +285,71 @@ def test_planted_mistakes_are_caught_by_brute_force(kind):
     good, _ = run(ref.brute_force_fp64, case)
     bad, _ = run(_mutant(kind), case)
     assert not np.allclose(bad, good, atol=1e-3)
+
+
+# ------------------------------------------------------------ CSR page lists, 16-bit KV siblings
+def _to_csr(table, lens, rng=None, pad=0):
+    """The reference benchmark's CSR form (``benchmark_cuda_paged_decode.py:67-73``):
+    ``page_indices`` = the used pages of each row, ``page_indptr`` = row offsets.
+    ``pad`` extra garbage entries between rows check that offsets, not row lengths, are used."""
+    rows, indptr = [], [0]
+    for b, L in enumerate(lens):
+        n = (int(L) + 15) // 16
+        rows.append(np.asarray(table[b, :n], dtype=np.int32))
+        if pad:
+            rows.append(np.full(pad, 10**6, dtype=np.int32))
+        indptr.append(indptr[-1] + n + pad)
+    return np.concatenate(rows) if rows else np.zeros(0, np.int32), np.asarray(indptr, dtype=np.int32)
+
+
+@pytest.mark.parametrize("spec", TINY[:3])
+def test_csr_page_list_equals_block_table(spec):
+    case = make_case(**spec)
+    exp = run(ref.reference, case)
+    for pad in (0, 3):
+        indices, indptr = _to_csr(case["block_table"], case["seq_lens"], pad=pad)
+        c = dict(case, block_table=indices)
+        got = run(ref.reference, c, page_indptr=indptr)
+        np.testing.assert_array_equal(got[0], exp[0])
+        np.testing.assert_array_equal(got[1], exp[1])
+
+
+def test_csr_with_shifted_offsets_is_caught():
+    """A planted off-by-one row offset (indptr[b + 1] for indptr[b]) must change the result."""
+    case = make_case(seed=9, batch=3, hq=4, hkv=2, d=64, lens=[40, 36, 33])  # 3 pages each
+    indices, indptr = _to_csr(case["block_table"], case["seq_lens"])
+    good = run(ref.reference, dict(case, block_table=indices), page_indptr=indptr)
+    shifted = np.concatenate([indptr[1:], indptr[-1:] + 3])
+    indices_padded = np.concatenate([indices, np.zeros(8, np.int32)])
+    bad = run(ref.reference, dict(case, block_table=indices_padded), page_indptr=shifted)
+    assert not np.allclose(good[0], bad[0])
+
+
+def test_dense_kv_reference_equals_fp8_path_on_representable_values():
+    """16-bit caches holding exactly the dequantised fp8 values (scale 1) reproduce the
+    fp8 oracle bit for bit; the fp8 oracle itself is pinned by the fp64 brute force."""
+    case = make_case(seed=12, batch=2, hq=8, hkv=2, d=128, lens=[70, 33], q_len=2)
+    k = ref.e4m3fn_to_f32(case["key_cache"])
+    v = ref.e4m3fn_to_f32(case["value_cache"])
+    exp = ref.reference(case["query"], case["key_cache"], case["value_cache"], case["block_table"],
+                        case["seq_lens"], 1.0, 1.0, q_len=2)
+    got = ref.reference_dense_kv(case["query"], k, v, case["block_table"], case["seq_lens"], q_len=2)
+    np.testing.assert_array_equal(got[0], exp[0])
+    np.testing.assert_array_equal(got[1], exp[1])
+    bf = ref.brute_force_fp64(case["query"], case["key_cache"], case["value_cache"], case["block_table"],
+                              case["seq_lens"], 1.0, 1.0, q_len=2)
+    np.testing.assert_allclose(got[0], bf[0], rtol=2e-5, atol=1e-3)  # values up to 448
+
+
+def test_dense_kv_single_token_and_equal_keys_closed_forms():
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 1, 1, 64)), 16, axis=1).astype(np.float32)  # 16 equal keys
+    v = rng.standard_normal((1, 16, 1, 64)).astype(np.float32)
+    table = np.zeros((1, 1), np.int32)
+    out, lse = ref.reference_dense_kv(q, k, v, table, np.array([1]))
+    np.testing.assert_allclose(out[0], np.broadcast_to(v[0, 0, 0], (2, 64)), rtol=1e-6)
+    out, lse = ref.reference_dense_kv(q, k, v, table, np.array([16]))
+    np.testing.assert_allclose(out[0], np.broadcast_to(v[0, :, 0].mean(0), (2, 64)), rtol=1e-5, atol=1e-6)
+    s = (q[0] @ k[0, 0, 0]) / 8.0
+    np.testing.assert_allclose(lse[0], s + math.log(16), rtol=1e-5)
