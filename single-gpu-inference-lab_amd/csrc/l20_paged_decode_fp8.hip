@@ -1487,6 +1487,12 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
 
 }  // namespace
 
+// Error reporting for the other translation units of the library.
+namespace l20pd_host {
+int32_t set_error(int32_t code, const char *msg) { return fail(code, msg); }
+void clear_error() { g_last_error[0] = '\0'; }
+}  // namespace l20pd_host
+
 extern "C" {
 
 int32_t l20_pd_abi_version(void) { return L20_PD_ABI_VERSION; }

@@ -26,6 +26,7 @@
 
 #include <optional>
 
+#include "l20_kv_write.h"
 #include "l20_paged_decode.h"
 
 namespace {
@@ -264,6 +265,131 @@ at::Tensor paged_decode_split_indices_out(const at::Tensor &query, const at::Ten
   return output;
 }
 
+// ---------------------------------------------------------------------------
+// Paged KV-cache producer: l20_rope_and_cache (integrations/vllm/l20_rope_kv.py:256-309)
+// with fp8 caches, and the fp8 scale helper.
+// ---------------------------------------------------------------------------
+l20_pd_kv_write_args kv_args(const std::optional<at::Tensor> &query, const at::Tensor &key, const at::Tensor &value,
+                             const at::Tensor &positions, const at::Tensor &cos_sin_cache, bool is_neox,
+                             const at::Tensor &key_cache, const at::Tensor &value_cache,
+                             const at::Tensor &slot_mapping) {
+  TORCH_CHECK(key.is_cuda(), "key must be CUDA");
+  TORCH_CHECK(key.scalar_type() == at::kBFloat16 || key.scalar_type() == at::kHalf,
+              "l20_rope_and_cache supports FP16 and BF16");
+  TORCH_CHECK(value.scalar_type() == key.scalar_type(), "Q, K, and V must use the same dtype");
+  TORCH_CHECK(key.dim() == 3 && value.dim() == 3, "Q, K, and V must be [tokens, heads, head_dim]");
+  TORCH_CHECK(key.sizes() == value.sizes(), "Q, K, and V shapes are incompatible");
+  const bool has_q = query.has_value() && query->defined();
+  if (has_q) {
+    TORCH_CHECK(query->scalar_type() == key.scalar_type(), "Q, K, and V must use the same dtype");
+    TORCH_CHECK(query->dim() == 3 && query->size(0) == key.size(0) && query->size(2) == key.size(2),
+                "Q, K, and V shapes are incompatible");
+    TORCH_CHECK(query->stride(2) == 1, "head_dim must be the contiguous dimension");
+    check_same_device(*query, key, "query");
+  }
+  TORCH_CHECK(key_cache.dim() == 4 && value_cache.sizes() == key_cache.sizes(),
+              "cache must use NHD [blocks, block, heads, dim]");
+  TORCH_CHECK(key_cache.size(1) == 16, "cache must use NHD [blocks, block, heads, dim]");
+  TORCH_CHECK(key_cache.size(2) == key.size(1) && key_cache.size(3) == key.size(2),
+              "cache head shape must match K/V");
+  const bool fp8 = key_cache.scalar_type() == at::kFloat8_e4m3fn;
+  TORCH_CHECK(fp8 || key_cache.scalar_type() == key.scalar_type(),
+              "K/V cache must be torch.float8_e4m3fn or the model dtype");
+  TORCH_CHECK(value_cache.scalar_type() == key_cache.scalar_type(), "K/V cache mismatch");
+  TORCH_CHECK(positions.scalar_type() == at::kLong && slot_mapping.scalar_type() == at::kLong,
+              "positions and slot_mapping must be int64");
+  TORCH_CHECK(positions.numel() == key.size(0) && slot_mapping.numel() == key.size(0),
+              "positions and slot_mapping must match token count");
+  TORCH_CHECK(positions.is_contiguous() && slot_mapping.is_contiguous(), "positions and slot_mapping must be contiguous");
+  TORCH_CHECK(cos_sin_cache.dim() == 2 && cos_sin_cache.stride(1) == 1, "invalid cos_sin_cache rotary dimension");
+  const int64_t rot = cos_sin_cache.size(1);
+  TORCH_CHECK(rot > 0 && rot <= key.size(2) && rot % 2 == 0, "invalid cos_sin_cache rotary dimension");
+  for (const at::Tensor *t : {&value, &positions, &cos_sin_cache, &key_cache, &value_cache, &slot_mapping})
+    check_same_device(*t, key, "every tensor");
+  TORCH_CHECK(key.stride(2) == 1 && value.stride(2) == 1 && key_cache.stride(3) == 1 && value_cache.stride(3) == 1,
+              "head_dim must be the contiguous dimension");
+  l20_pd_kv_write_args a{};
+  if (has_q) {
+    a.query = query->data_ptr();
+    a.q_stride_token = query->stride(0);
+    a.q_stride_head = query->stride(1);
+    a.num_q_heads = (int32_t)query->size(1);
+  }
+  a.key = key.data_ptr();
+  a.k_stride_token = key.stride(0);
+  a.k_stride_head = key.stride(1);
+  a.value = value.data_ptr();
+  a.v_stride_token = value.stride(0);
+  a.v_stride_head = value.stride(1);
+  a.dtype = dtype_code(key);
+  a.positions = positions.data_ptr<int64_t>();
+  a.cos_sin_cache = cos_sin_cache.data_ptr();
+  a.cs_stride_position = cos_sin_cache.stride(0);
+  a.cs_dtype = dtype_code(cos_sin_cache);
+  a.rotary_dim = (int32_t)rot;
+  a.is_neox = is_neox ? 1 : 0;
+  a.slot_mapping = slot_mapping.data_ptr<int64_t>();
+  a.key_cache = key_cache.data_ptr();
+  a.kc_stride_page = key_cache.stride(0);
+  a.kc_stride_token = key_cache.stride(1);
+  a.kc_stride_head = key_cache.stride(2);
+  a.value_cache = value_cache.data_ptr();
+  a.vc_stride_page = value_cache.stride(0);
+  a.vc_stride_token = value_cache.stride(1);
+  a.vc_stride_head = value_cache.stride(2);
+  a.num_pages = key_cache.size(0);
+  a.cache_dtype = fp8 ? L20_PD_KV_FP8_E4M3 : (key.scalar_type() == at::kBFloat16 ? L20_PD_KV_BF16 : L20_PD_KV_FP16);
+  a.k_scale = 1.0f;
+  a.v_scale = 1.0f;
+  a.num_tokens = (int32_t)key.size(0);
+  a.num_kv_heads = (int32_t)key.size(1);
+  a.head_dim = (int32_t)key.size(2);
+  return a;
+}
+
+const float *per_head_scale(const std::optional<at::Tensor> &t, const at::Tensor &key) {
+  if (!t.has_value() || !t->defined()) return nullptr;
+  TORCH_CHECK(t->scalar_type() == at::kFloat && t->is_contiguous() && t->numel() == key.size(1),
+              "per-head scales must be contiguous fp32 [num_kv_heads]");
+  check_same_device(*t, key, "per-head scales");
+  return t->data_ptr<float>();
+}
+
+void rope_and_cache(const std::optional<at::Tensor> &query, const at::Tensor &key, const at::Tensor &value,
+                    const at::Tensor &positions, const at::Tensor &cos_sin_cache, bool is_neox,
+                    const at::Tensor &key_cache, const at::Tensor &value_cache, const at::Tensor &slot_mapping,
+                    double k_scale, double v_scale, const std::optional<at::Tensor> &k_scale_per_head,
+                    const std::optional<at::Tensor> &v_scale_per_head) {
+  l20_pd_kv_write_args a =
+      kv_args(query, key, value, positions, cos_sin_cache, is_neox, key_cache, value_cache, slot_mapping);
+  a.k_scale = (float)k_scale;
+  a.v_scale = (float)v_scale;
+  a.k_scale_per_head = per_head_scale(k_scale_per_head, key);
+  a.v_scale_per_head = per_head_scale(v_scale_per_head, key);
+  const c10::DeviceGuard guard(key.device());
+  void *stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
+  const int32_t rc = l20_pd_rope_and_cache(&a, stream);
+  TORCH_CHECK(rc == L20_PD_OK, l20_pd_last_error());
+}
+
+void kv_fp8_scales(const at::Tensor &key, const at::Tensor &value, const at::Tensor &positions,
+                   const at::Tensor &cos_sin_cache, bool is_neox, const at::Tensor &key_cache,
+                   const at::Tensor &value_cache, const at::Tensor &slot_mapping, const at::Tensor &k_scales,
+                   const at::Tensor &v_scales, bool per_head) {
+  const l20_pd_kv_write_args a =
+      kv_args(std::nullopt, key, value, positions, cos_sin_cache, is_neox, key_cache, value_cache, slot_mapping);
+  for (const at::Tensor *t : {&k_scales, &v_scales}) {
+    TORCH_CHECK(t->scalar_type() == at::kFloat && t->is_contiguous() && t->numel() == key.size(1),
+                "scale outputs must be contiguous fp32 [num_kv_heads]");
+    check_same_device(*t, key, "scale outputs");
+  }
+  const c10::DeviceGuard guard(key.device());
+  void *stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
+  const int32_t rc =
+      l20_pd_kv_fp8_scales(&a, k_scales.data_ptr<float>(), v_scales.data_ptr<float>(), per_head ? 1 : 0, stream);
+  TORCH_CHECK(rc == L20_PD_OK, l20_pd_last_error());
+}
+
 }  // namespace
 
 TORCH_LIBRARY(l20_stack, m) {
@@ -296,9 +422,20 @@ TORCH_LIBRARY(l20_stack, m) {
       "int max_seq_len, int split_size, "
       "float? softmax_scale=None, int q_len=1, "
       "Tensor(e!)? lse=None) -> Tensor(d!)");
+  m.def(
+      "rope_and_cache(Tensor(a!)? query, Tensor(b!) key, Tensor value, Tensor positions, "
+      "Tensor cos_sin_cache, bool is_neox, Tensor(c!) key_cache, Tensor(d!) value_cache, "
+      "Tensor slot_mapping, float k_scale=1.0, float v_scale=1.0, "
+      "Tensor? k_scale_per_head=None, Tensor? v_scale_per_head=None) -> ()");
+  m.def(
+      "kv_fp8_scales(Tensor key, Tensor value, Tensor positions, Tensor cos_sin_cache, bool is_neox, "
+      "Tensor key_cache, Tensor value_cache, Tensor slot_mapping, Tensor(a!) k_scales, "
+      "Tensor(b!) v_scales, bool per_head=True) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(l20_stack, CUDA, m) {
+  m.impl("rope_and_cache", &rope_and_cache);
+  m.impl("kv_fp8_scales", &kv_fp8_scales);
   m.impl("paged_decode_split_out", &paged_decode_split_out);
   m.impl("paged_decode_fp8_e4m3_split_out", &paged_decode_fp8_e4m3_split_out);
   m.impl("paged_decode_split_indices_out", &paged_decode_split_indices_out);

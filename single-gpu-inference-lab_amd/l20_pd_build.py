@@ -26,6 +26,8 @@ INCLUDE = ROOT / "include"
 HIP_LIB = HERE / "libl20_paged_decode_hip.so"
 OPS_LIB = HERE / "l20_paged_decode_ops.so"
 ARCH = os.environ.get("L20_PD_ARCH", "gfx950")
+# The decode kernels and the paged KV-cache producer, one shared object.
+HIP_SOURCES = [CSRC / "l20_paged_decode_fp8.hip", CSRC / "l20_kv_write.hip"]
 
 # Packed-FP32 VALU forms are kept out of every HIP build.
 HIP_FLAGS = [
@@ -55,7 +57,7 @@ def _run(cmd, verbose: bool) -> None:
 
 def build_hip_library(verbose: bool = False) -> Path:
     tmp = HIP_LIB.with_suffix(".so.tmp")
-    _run([_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", CSRC / "l20_paged_decode_fp8.hip", "-o", tmp], verbose)
+    _run([_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", *HIP_SOURCES, "-o", tmp], verbose)
     os.replace(tmp, HIP_LIB)
     return HIP_LIB
 

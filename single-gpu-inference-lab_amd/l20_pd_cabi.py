@@ -1,4 +1,4 @@
-"""ctypes binding of the C ABI in ``include/l20_paged_decode.h``.
+"""ctypes binding of the C ABI in ``include/l20_paged_decode.h`` and ``include/l20_kv_write.h``.
 
 Loads ``libl20_paged_decode_hip.so`` from beside this file and mirrors the
 ``l20_pd_fp8_args`` struct field by field.  ``args_from_tensors`` fills the
@@ -19,7 +19,7 @@ L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
 L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16 = 0, 1, 2
 ABI_VERSION = 2
 
-# Every extern "C" symbol declared in include/l20_paged_decode.h.
+# Every extern "C" symbol declared in include/*.h.
 EXPORTED = (
     "l20_pd_abi_version",
     "l20_pd_last_error",
@@ -34,6 +34,9 @@ EXPORTED = (
     "l20_pd_fp8_e4m3_dequant_bf16",
     "l20_pd_stream_read",
     "l20_pd_stream_copy",
+    "l20_pd_kv_write_check",
+    "l20_pd_rope_and_cache",
+    "l20_pd_kv_fp8_scales",
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -60,6 +63,25 @@ class L20PdFp8Args(ctypes.Structure):
         ("batch", _i32), ("q_len", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
         ("max_seq_len", _i32), ("split_size", _i32),
         ("kv_dtype", _i32), ("page_indptr", _vp),
+    ]
+
+
+class L20PdKvWriteArgs(ctypes.Structure):
+    """Mirror of ``l20_pd_kv_write_args`` (include/l20_kv_write.h)."""
+
+    _fields_ = [
+        ("query", _vp), ("q_stride_token", _i64), ("q_stride_head", _i64), ("num_q_heads", _i32),
+        ("key", _vp), ("k_stride_token", _i64), ("k_stride_head", _i64),
+        ("value", _vp), ("v_stride_token", _i64), ("v_stride_head", _i64),
+        ("dtype", _i32),
+        ("positions", _vp), ("cos_sin_cache", _vp), ("cs_stride_position", _i64), ("cs_dtype", _i32),
+        ("rotary_dim", _i32), ("is_neox", _i32),
+        ("slot_mapping", _vp),
+        ("key_cache", _vp), ("kc_stride_page", _i64), ("kc_stride_token", _i64), ("kc_stride_head", _i64),
+        ("value_cache", _vp), ("vc_stride_page", _i64), ("vc_stride_token", _i64), ("vc_stride_head", _i64),
+        ("num_pages", _i64), ("cache_dtype", _i32),
+        ("k_scale", _f32), ("v_scale", _f32), ("k_scale_per_head", _vp), ("v_scale_per_head", _vp),
+        ("num_tokens", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
     ]
 
 
@@ -96,6 +118,13 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     lib.l20_pd_stream_read.restype = _i32
     lib.l20_pd_stream_copy.argtypes = [_vp, _vp, _i64, _i32, _vp]
     lib.l20_pd_stream_copy.restype = _i32
+    kv_p = ctypes.POINTER(L20PdKvWriteArgs)
+    lib.l20_pd_kv_write_check.argtypes = [kv_p]
+    lib.l20_pd_kv_write_check.restype = _i32
+    lib.l20_pd_rope_and_cache.argtypes = [kv_p, _vp]
+    lib.l20_pd_rope_and_cache.restype = _i32
+    lib.l20_pd_kv_fp8_scales.argtypes = [kv_p, _vp, _vp, _i32, _vp]
+    lib.l20_pd_kv_fp8_scales.restype = _i32
     if path is None:
         _lib = lib
     return lib

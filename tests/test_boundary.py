@@ -26,8 +26,11 @@ REFERENCE_SCHEMA_PREFIX = (
 
 
 def header_functions():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(l20_pd_\w+)\s*\(", text, re.M)))
+    """Every function declared in include/*.h."""
+    names = set()
+    for header in sorted(HEADER.parent.glob("*.h")):
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(l20_pd_\w+)\s*\(", header.read_text(), re.M))
+    return sorted(names)
 
 
 def test_library_exports_every_header_symbol():
