@@ -1,0 +1,1 @@
+"""Stand-in package tree for the ROCm install-hook tests (not vLLM code)."""
