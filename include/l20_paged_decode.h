@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define L20_PD_ABI_VERSION 2
+#define L20_PD_ABI_VERSION 3
 
 /* Element types for query/output and the partial-output workspace. */
 enum l20_pd_dtype {
@@ -128,6 +128,13 @@ typedef struct l20_pd_fp8_args {
   /* ABI version 2 */
   int32_t kv_dtype;                /* enum l20_pd_kv_dtype */
   const int32_t *page_indptr;      /* CSR row offsets [batch+1], or NULL for block_table rows */
+
+  /* ABI version 3: tree (ancestor-mask) verification.  tree_mask[b * stride + i]
+   * (int32, bit j) lets query row b*q_len+i see key seq_lens[b]-q_len+j; the keys
+   * before the newest q_len stay visible to every row.  NULL keeps the causal
+   * rule (row i sees those keys up to its own).  stride 0 shares one mask. */
+  const int32_t *tree_mask;
+  int64_t tree_mask_stride_batch;
 } l20_pd_fp8_args;
 
 /* ABI version of the loaded library (L20_PD_ABI_VERSION). */

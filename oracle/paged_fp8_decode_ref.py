@@ -169,6 +169,20 @@ def dequantize(codes: np.ndarray, scale: ScaleLike, head_axis: int = -2) -> np.n
     return (values * scales.reshape(shape)).astype(np.float32)
 
 
+def _tree_row(tree_mask: Optional[np.ndarray], b: int) -> Optional[np.ndarray]:
+    if tree_mask is None:
+        return None
+    tm = np.asarray(tree_mask)
+    return tm if tm.ndim == 1 else tm[b]
+
+
+def tree_bits_from_mask(ancestor_mask: np.ndarray) -> np.ndarray:
+    """Boolean ancestor matrix [..., S, S] (row i sees draft j) -> int64 bitmasks [..., S]."""
+    m = np.asarray(ancestor_mask, dtype=bool)
+    weights = (np.int64(1) << np.arange(m.shape[-1], dtype=np.int64))
+    return (m.astype(np.int64) * weights).sum(-1)
+
+
 def table_row(block_table: np.ndarray, b: int, page_indptr: Optional[np.ndarray] = None) -> np.ndarray:
     """Page list of sequence ``b``: row ``b`` of a ``[B, max_pages]`` block table, or
     ``page_indices[indptr[b]:indptr[b+1]]`` of a CSR page list
@@ -178,10 +192,30 @@ def table_row(block_table: np.ndarray, b: int, page_indptr: Optional[np.ndarray]
     return np.asarray(block_table)[int(page_indptr[b]):int(page_indptr[b + 1])]
 
 
+def tree_visibility(length: int, q_len: int, tree_bits: Optional[np.ndarray]) -> np.ndarray:
+    """[q_len, L] visibility of one sequence's keys.  Without ``tree_bits`` row ``i``
+    sees keys ``0 .. L - q_len + i`` (causal among the newest ``q_len``); with the
+    per-row ancestor bitmasks ``tree_bits`` [q_len] row ``i`` sees the prefix
+    ``0 .. L - q_len - 1`` and draft key ``L - q_len + j`` iff bit ``j`` of
+    ``tree_bits[i]`` is set (``triton_tree_attention.py:1218-1240``: the cached
+    prefix plus the ancestor mask over the suffix)."""
+    token = np.arange(length)
+    base = length - q_len
+    if tree_bits is None:
+        limit = base + np.arange(q_len)
+        return token[None, :] <= limit[:, None]
+    bits = np.asarray(tree_bits, dtype=np.int64).reshape(q_len, 1) & 0xFFFFFFFF
+    draft = token[None, :] - base
+    in_draft = draft >= 0
+    bit = (bits >> np.clip(draft, 0, 31)) & 1
+    return np.where(in_draft, bit == 1, True)
+
+
 def _attend(query_rows: np.ndarray, keys: np.ndarray, values: np.ndarray, num_kv_heads: int,
-            scale: float, q_len: int, acc_dtype) -> Tuple[np.ndarray, np.ndarray]:
-    """Softmax attention of one sequence's ``q_len`` query rows over its ``L`` keys;
-    row ``i`` sees keys ``0 .. L - q_len + i``.  Returns (out [q, Hq, D], lse [q, Hq])."""
+            scale: float, q_len: int, acc_dtype, tree_bits: Optional[np.ndarray] = None
+            ) -> Tuple[np.ndarray, np.ndarray]:
+    """Softmax attention of one sequence's ``q_len`` query rows over its ``L`` keys with
+    the visibility of ``tree_visibility``.  Returns (out [q, Hq, D], lse [q, Hq])."""
     length = keys.shape[0]
     _, num_q_heads, head_dim = query_rows.shape
     group = num_q_heads // num_kv_heads
@@ -190,9 +224,7 @@ def _attend(query_rows: np.ndarray, keys: np.ndarray, values: np.ndarray, num_kv
     # [q, Hkv, G, D] x [L, Hkv, D] -> [q, Hkv, G, L]
     q = query_rows.reshape(q_len, num_kv_heads, group, head_dim)
     scores = np.einsum("ihgd,thd->ihgt", q.astype(acc_dtype), keys) * acc_dtype(scale)
-    token = np.arange(length)
-    limit = length - q_len + np.arange(q_len)  # last visible key per row
-    visible = token[None, :] <= limit[:, None]  # [q, L]
+    visible = tree_visibility(length, q_len, tree_bits)  # [q, L]
     scores = np.where(visible[:, None, None, :], scores, -np.inf)
     row_max = scores.max(axis=-1, keepdims=True)
     safe_max = np.where(np.isfinite(row_max), row_max, 0.0)
@@ -221,6 +253,7 @@ def reference(
     acc_dtype: np.dtype = np.float32,
     rows: Optional[Sequence[int]] = None,
     page_indptr: Optional[np.ndarray] = None,
+    tree_mask: Optional[np.ndarray] = None,
 ) -> Tuple[np.ndarray, np.ndarray]:
     """Dequantise-then-attend (``smoke_cuda_paged_fp8_decode_op.py:22-41``).
 
@@ -232,6 +265,8 @@ def reference(
     Returns ``(out [B*q_len, Hq, D] float32, lse [B*q_len, Hq] float32)``;
     rows with no visible key give zeros and ``lse = -inf``.
     ``rows`` restricts the work to the listed batch entries (others stay 0).
+    ``tree_mask`` [B, q_len] (or [q_len], shared) int bitmasks replace the causal
+    rule with an ancestor mask over the newest ``q_len`` keys.
     """
     query = np.asarray(query, dtype=np.float32)
     n_rows, num_q_heads, head_dim = query.shape
@@ -250,7 +285,8 @@ def reference(
         if round_kv_to is not None:
             keys = keys.astype(round_kv_to).astype(np.float32)
             values = values.astype(round_kv_to).astype(np.float32)
-        o, l = _attend(query[b * q_len:(b + 1) * q_len], keys, values, num_kv_heads, scale, q_len, acc_dtype)
+        o, l = _attend(query[b * q_len:(b + 1) * q_len], keys, values, num_kv_heads, scale, q_len, acc_dtype,
+                       _tree_row(tree_mask, b))
         out[b * q_len:(b + 1) * q_len] = o
         lse[b * q_len:(b + 1) * q_len] = l
     return out, lse
@@ -267,6 +303,7 @@ def reference_dense_kv(
     q_len: int = 1,
     rows: Optional[Sequence[int]] = None,
     page_indptr: Optional[np.ndarray] = None,
+    tree_mask: Optional[np.ndarray] = None,
 ) -> Tuple[np.ndarray, np.ndarray]:
     """The fp16/bf16-KV siblings (``smoke_cuda_paged_decode_op.py:13-29``,
     ``l20_paged_decode.cu:156-289``): the same attention over caches whose values are
@@ -285,7 +322,8 @@ def reference_dense_kv(
         pages = table_row(block_table, b, page_indptr)
         keys = np.asarray(gather_pages(key_cache, pages, length), dtype=np.float32)
         values = np.asarray(gather_pages(value_cache, pages, length), dtype=np.float32)
-        o, l = _attend(query[b * q_len:(b + 1) * q_len], keys, values, num_kv_heads, scale, q_len, np.float32)
+        o, l = _attend(query[b * q_len:(b + 1) * q_len], keys, values, num_kv_heads, scale, q_len, np.float32,
+                       _tree_row(tree_mask, b))
         out[b * q_len:(b + 1) * q_len] = o
         lse[b * q_len:(b + 1) * q_len] = l
     return out, lse
@@ -363,6 +401,7 @@ def brute_force_fp64(
     *,
     softmax_scale: Optional[float] = None,
     q_len: int = 1,
+    tree_mask: Optional[np.ndarray] = None,
 ) -> Tuple[np.ndarray, np.ndarray]:
     """Scalar float64 loops, written independently of ``reference``; tiny inputs only."""
     n_rows, num_q_heads, head_dim = np.asarray(query).shape
@@ -378,10 +417,15 @@ def brute_force_fp64(
         b, i = divmod(r, q_len)
         length = int(seq_lens[b])
         last = length - q_len + i
+        if tree_mask is None:
+            keys = list(range(last + 1))
+        else:  # prefix, then the draft keys whose bit is set in row i's ancestor word
+            word = int(np.asarray(tree_mask).reshape(-1, q_len)[0 if np.asarray(tree_mask).ndim == 1 else b][i])
+            keys = [t for t in range(length) if t < length - q_len or (word >> (t - (length - q_len))) & 1]
         for h in range(num_q_heads):
             kvh = h // group
             scores = []
-            for t in range(last + 1):
+            for t in keys:
                 page = int(block_table[b][t // PAGE_SIZE])
                 slot = t % PAGE_SIZE
                 dot = 0.0
@@ -395,7 +439,7 @@ def brute_force_fp64(
             weights = [math.exp(s - top) for s in scores]
             total = sum(weights)
             lse[r, h] = top + math.log(total)
-            for t, w in enumerate(weights):
+            for t, w in zip(keys, weights):
                 page = int(block_table[b][t // PAGE_SIZE])
                 slot = t % PAGE_SIZE
                 for d in range(head_dim):

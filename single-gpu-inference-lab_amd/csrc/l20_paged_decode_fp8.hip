@@ -2,7 +2,7 @@
 //
 // Two kernels per call, both enqueued on the caller's stream:
 //
-//  pd_fp8_partial<QT, D, NQT>   persistent: CUs x occupancy workgroups, one
+//  pd_fp8_partial<QT, KT, D, NQT, TREE>  persistent: CUs x occupancy workgroups, one
 //    wave per KV head (W waves, W the largest divisor of Hkv up to 8).
 //    A work item is one (sequence, split) pair; every wave of the workgroup
 //    computes attention for ALL query rows of its KV head (GQA group x
@@ -101,6 +101,8 @@ struct PartialParams {
   int bt_pages;  // block-table row length
   int compact;   // queue items numbered through an LDS prefix
   const int32_t *indptr;  // CSR page list: sequence b's pages are bt[indptr[b] .. indptr[b + 1])
+  const int32_t *tree;    // ancestor words [b * tree_sb + i] (bit j: row i sees draft key j), or NULL
+  int64_t tree_sb;
 };
 
 // ---------------------------------------------------------------------------
@@ -267,7 +269,7 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // An item of a single-split sequence writes the final output and LSE (and
 // marks split slot 0 with +inf for the merge); any other item writes its
 // fp32 partial (o / l, m, l) at its split slot.
-template <typename QT, int KT, int D, int NQT>
+template <typename QT, int KT, int D, int NQT, bool TREE>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
   typedef typename KvBlock<KT, D>::type Block;
@@ -337,6 +339,19 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     return v;
   };
   // Query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16.
+  // Tree verification: ancestor words of this lane's query columns over the
+  // newest q_len keys (bit j lets the column see key L - q_len + j).  The
+  // causal rule (TREE = false) keeps no words: its limit is recomputed per
+  // unit, which keeps the tree state out of the causal kernels' registers.
+  auto load_tree = [&](int b, int (&dst)[TREE ? NQT : 1]) {
+    if constexpr (TREE) {
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        const int col = 16 * qt + n16;
+        dst[qt] = col < mcols ? p.tree[(int64_t)b * p.tree_sb + (col % q_len)] : 0;
+      }
+    }
+  };
   auto load_q = [&](int b, int kvh, qvec8 (&dst)[NQT][NS]) {
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
@@ -417,6 +432,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   qvec8 qop[NQT][NS];
   qvec8 qopN[kQPrefetch ? NQT : 1][NS];
   int pidU = -1;
+  int treeU[TREE ? NQT : 1];                    // ancestor words of the current unit
+  int treeN[TREE && kQPrefetch ? NQT : 1];      // ... and of the next (prefetched with its query)
   int par = 0;         // block k of the current unit is in buf[(k + par) & 1]
   int issuedU = 0;     // blocks of the current unit already loading
   bool u_loaded = false;  // page ids and query of the current unit are loading
@@ -441,6 +458,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       if (nU > 1) load_block(buf[1], pidU, wave, 1);
       issuedU = min(nU, 2);
       load_q(cb, wave, qop);
+      load_tree(cb, treeU);
       u_loaded = true;
     } else {
       cb = -2;  // hole: the workgroup starts on the queue
@@ -628,6 +646,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       if (!u_loaded) {
         pidU = load_pid(b, split, L);
         load_q(b, kvh, qop);
+        load_tree(b, treeU);
         issuedU = 0;
       }
       // top up the unit's first two blocks
@@ -658,8 +677,12 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           nN = n_blocks(ns, nL);
           pidN = load_pid(nb, ns, nL);
         }
-        if constexpr (kQPrefetch)
-          if (hasN) load_q(nB, nKvh, qopN);
+        if constexpr (kQPrefetch) {
+          if (hasN) {
+            load_q(nB, nKvh, qopN);
+            load_tree(nB, treeN);
+          }
+        }
       };
       // In the last unit the successor is claimed kClaimLead blocks and
       // published kPublishLead blocks before the end (at the start of a
@@ -676,14 +699,17 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
       const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
       const float c_log2 = k_scale * p.qk_scale_log2;
-      // ---- masking limits: last visible token for this lane's column ----
-      int lim[NQT];
+      // ---- masking: keys before draft0 are visible to every column; key
+      // draft0 + j to draft row i when j <= i (causal) or when bit j of the
+      // row's ancestor word is set (TREE) ----
+      const int draft0 = L - q_len;  // first key of the newest q_len
+      int lim[TREE ? 1 : NQT];       // causal: last visible key of the lane's column
+      if constexpr (!TREE) {
 #pragma unroll
-      for (int qt = 0; qt < NQT; ++qt) {
-        const int col = 16 * qt + n16;
-        lim[qt] = min(uEnd - 1, L - q_len + (col % q_len));
+        for (int qt = 0; qt < NQT; ++qt) lim[qt] = min(uEnd - 1, draft0 + (16 * qt + n16) % q_len);
       }
-      const int min_lim = min(uEnd - 1, L - q_len);
+      // the last key that every column sees
+      const int min_lim = min(uEnd - 1, TREE ? draft0 - 1 : draft0);
 
       f32x4 acc[NQT][NT];
       float m_run[NQT], l_run[NQT];
@@ -770,7 +796,12 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
               const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-              x[e] = (t <= lim[qt] && !((e >> 2) ? bad1 : bad0)) ? x[e] : -INFINITY;
+              bool vis;
+              if constexpr (TREE)
+                vis = t < uEnd && (t < draft0 || (((uint32_t)treeU[qt] >> ((t - draft0) & 31)) & 1u));
+              else
+                vis = t <= lim[qt];
+              x[e] = (vis && !((e >> 2) ? bad1 : bad0)) ? x[e] : -INFINITY;
             }
           }
           float mloc = x[0];
@@ -894,7 +925,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         if (k < nU) step(buf[0], k);
       }
       if constexpr (!kQPrefetch)
-        if (hasN) load_q(nB, nKvh, qop);  // qop is dead once the last block is computed
+        if (hasN) {
+          load_q(nB, nKvh, qop);  // qop and treeU are dead once the last block is computed
+          load_tree(nB, treeU);
+        }
 
       // ---- epilogue: this lane holds column 16*qt + lane%16, dims [DPL*j, DPL*j + DPL) ----
 #pragma unroll
@@ -968,6 +1002,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // ---- the next unit inherits the stream ----
       par = (par + nU) & 1;
       pidU = pidN;
+      if constexpr (TREE && kQPrefetch) treeU[0] = treeN[0];
       issuedU = issuedN;
       u_loaded = hasN;
       if constexpr (kQPrefetch) {
@@ -1224,6 +1259,8 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (!a->query || !a->key_cache || !a->value_cache || !a->block_table || !a->seq_lens || !a->output)
     return fail(L20_PD_EINVAL, "null tensor pointer");
   if (((uintptr_t)a->page_indptr % 4) != 0) return fail(L20_PD_EINVAL, "page_indptr must be int32-aligned");
+  if (((uintptr_t)a->tree_mask % 4) != 0 || a->tree_mask_stride_batch < 0)
+    return fail(L20_PD_EINVAL, "tree_mask must be int32 [batch, q_len] (batch stride >= 0)");
   if (a->num_pages <= 0) return fail(L20_PD_EINVAL, "K/V cache has no pages");
   const int32_t n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
   if (n_s > 1) {
@@ -1279,16 +1316,17 @@ bool partial_compact(int batch) { return batch <= l20pd::kMaxCompactBatch; }
 // at the kernel's occupancy, never more than there are split-major slots.
 // L20_PD_MAX_WORKGROUPS (a positive integer) caps the count, which lets tests
 // drive many items through each workgroup.
-template <typename QT, int KT, int D, int NQT>
+template <typename QT, int KT, int D, int NQT, bool TREE>
 int partial_grid(int threads, size_t lds, int64_t max_items) {
-  static thread_local int cached_dev = -1, cached_threads = -1, cached_blocks = 0;
+  static thread_local int cached_dev = -1, cached_threads = -1, cached_blocks = 0;  // per instantiation
   static thread_local size_t cached_lds = 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   if (dev != cached_dev || threads != cached_threads || lds != cached_lds) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, KT, D, NQT>, threads, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE>, threads,
+                                                     lds) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
@@ -1305,26 +1343,33 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, max_items));
 }
 
-template <typename QT, int KT, int D, int NQT>
+template <typename QT, int KT, int D, int NQT, bool TREE>
 hipError_t launch_partial(l20pd::PartialParams pp, int batch, int num_kv_heads, hipStream_t stream) {
   const int nwaves = partial_waves(num_kv_heads);
   const int threads = 64 * nwaves;
   pp.compact = partial_compact(batch) ? 1 : 0;
   const size_t lds = pp.compact ? (size_t)(2 * batch + 1) * sizeof(int) : 0;
   const int64_t max_items = (int64_t)batch * pp.num_splits;
-  const int grid = partial_grid<QT, KT, D, NQT>(threads, lds, max_items);
-  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, KT, D, NQT>), dim3(grid), dim3(threads), lds, stream, pp);
+  const int grid = partial_grid<QT, KT, D, NQT, TREE>(threads, lds, max_items);
+  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE>), dim3(grid), dim3(threads), lds, stream, pp);
   return hipGetLastError();
+}
+
+template <typename QT, int KT, bool TREE>
+hipError_t launch_partial_mask(const l20pd::PartialParams &pp, int head_dim, int nqt, int batch, int num_kv_heads,
+                               hipStream_t stream) {
+  if (head_dim == 128)
+    return nqt == 1 ? launch_partial<QT, KT, 128, 1, TREE>(pp, batch, num_kv_heads, stream)
+                    : launch_partial<QT, KT, 128, 2, TREE>(pp, batch, num_kv_heads, stream);
+  return nqt == 1 ? launch_partial<QT, KT, 64, 1, TREE>(pp, batch, num_kv_heads, stream)
+                  : launch_partial<QT, KT, 64, 2, TREE>(pp, batch, num_kv_heads, stream);
 }
 
 template <typename QT, int KT>
 hipError_t launch_partial_shape(const l20pd::PartialParams &pp, int head_dim, int nqt, int batch, int num_kv_heads,
                                 hipStream_t stream) {
-  if (head_dim == 128)
-    return nqt == 1 ? launch_partial<QT, KT, 128, 1>(pp, batch, num_kv_heads, stream)
-                    : launch_partial<QT, KT, 128, 2>(pp, batch, num_kv_heads, stream);
-  return nqt == 1 ? launch_partial<QT, KT, 64, 1>(pp, batch, num_kv_heads, stream)
-                  : launch_partial<QT, KT, 64, 2>(pp, batch, num_kv_heads, stream);
+  return pp.tree ? launch_partial_mask<QT, KT, true>(pp, head_dim, nqt, batch, num_kv_heads, stream)
+                 : launch_partial_mask<QT, KT, false>(pp, head_dim, nqt, batch, num_kv_heads, stream);
 }
 
 template <typename QT, int D>
@@ -1401,6 +1446,8 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.batch = a.batch;
   pp.bt_pages = a.bt_max_pages;
   pp.indptr = a.page_indptr;
+  pp.tree = a.tree_mask;
+  pp.tree_sb = a.tree_mask_stride_batch;
   return pp;
 }
 

@@ -9,6 +9,8 @@
 //   Tensor? v_scale_per_head=None    (fp32 [Hkv]; overrides v_scale)
 //   int q_len=1                      (query rows [B*q_len, Hq, D], causal)
 //   Tensor(e!)? lse=None             (fp32 [B*q_len, Hq], natural log)
+//   Tensor? tree_mask=None           (int32 [B, q_len] or [q_len] ancestor bitmasks over the
+//                                     newest q_len keys: speculative tree verification)
 // paged_decode_split_out (fp16/bf16 caches; schema :121-127) appends
 // softmax_scale, q_len and lse the same way; paged_decode_split_indices_out
 // is the CSR page-list variant the reference exports through pybind
@@ -61,7 +63,8 @@ l20_pd_fp8_args make_args(const at::Tensor &query, const at::Tensor &key_cache, 
                           const PageTable &pages, const at::Tensor &seq_lens, const at::Tensor &partial_output,
                           const at::Tensor &partial_max, const at::Tensor &partial_sum, const at::Tensor &output,
                           int64_t max_seq_len, int64_t split_size, std::optional<double> softmax_scale, int64_t q_len,
-                          const std::optional<at::Tensor> &lse, int32_t kv_dtype) {
+                          const std::optional<at::Tensor> &lse, int32_t kv_dtype,
+                          const std::optional<at::Tensor> &tree_mask) {
   TORCH_CHECK(query.dim() == 3, "invalid query");
   TORCH_CHECK(key_cache.dim() == 4 && key_cache.size(3) == query.size(2), "NHD cache only");
   TORCH_CHECK(key_cache.sizes() == value_cache.sizes(), "K/V cache mismatch");
@@ -178,6 +181,15 @@ l20_pd_fp8_args make_args(const at::Tensor &query, const at::Tensor &key_cache, 
   a.max_seq_len = (int32_t)max_seq_len;
   a.split_size = (int32_t)split_size;
   a.kv_dtype = kv_dtype;
+  if (tree_mask.has_value() && tree_mask->defined()) {
+    const at::Tensor &t = *tree_mask;
+    TORCH_CHECK(t.scalar_type() == at::kInt && t.size(-1) == q_len && t.stride(-1) == 1 &&
+                    ((t.dim() == 1) || (t.dim() == 2 && t.size(0) == batch)),
+                "tree_mask must be int32 [batch, q_len] or [q_len] ancestor bitmasks");
+    check_same_device(t, query, "tree_mask");
+    a.tree_mask = t.data_ptr<int32_t>();
+    a.tree_mask_stride_batch = t.dim() == 2 ? t.stride(0) : 0;
+  }
   return a;
 }
 
@@ -208,13 +220,13 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
     const at::Tensor &partial_max, const at::Tensor &partial_sum, const at::Tensor &output, double k_scale,
     double v_scale, int64_t max_seq_len, int64_t split_size, std::optional<double> softmax_scale,
     const std::optional<at::Tensor> &k_scale_per_head, const std::optional<at::Tensor> &v_scale_per_head,
-    int64_t q_len, const std::optional<at::Tensor> &lse) {
+    int64_t q_len, const std::optional<at::Tensor> &lse, const std::optional<at::Tensor> &tree_mask) {
   check_query(query);
   TORCH_CHECK(key_cache.scalar_type() == at::kFloat8_e4m3fn && value_cache.scalar_type() == at::kFloat8_e4m3fn,
               "K/V cache must be torch.float8_e4m3fn");
   l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&block_table, nullptr}, seq_lens,
                                 partial_output, partial_max, partial_sum, output, max_seq_len, split_size,
-                                softmax_scale, q_len, lse, L20_PD_KV_FP8_E4M3);
+                                softmax_scale, q_len, lse, L20_PD_KV_FP8_E4M3, tree_mask);
   for (int which = 0; which < 2; ++which) {
     const auto &opt = which == 0 ? k_scale_per_head : v_scale_per_head;
     if (opt.has_value() && opt->defined()) {
@@ -237,12 +249,12 @@ at::Tensor paged_decode_split_out(const at::Tensor &query, const at::Tensor &key
                                   const at::Tensor &partial_output, const at::Tensor &partial_max,
                                   const at::Tensor &partial_sum, const at::Tensor &output, int64_t max_seq_len,
                                   int64_t split_size, std::optional<double> softmax_scale, int64_t q_len,
-                                  const std::optional<at::Tensor> &lse) {
+                                  const std::optional<at::Tensor> &lse, const std::optional<at::Tensor> &tree_mask) {
   check_query(query);
   const int32_t kv = check_16bit_cache(query, key_cache, value_cache);
   const l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&block_table, nullptr}, seq_lens,
                                       partial_output, partial_max, partial_sum, output, max_seq_len, split_size,
-                                      softmax_scale, q_len, lse, kv);
+                                      softmax_scale, q_len, lse, kv, tree_mask);
   launch(query, a, false);
   return output;
 }
@@ -255,12 +267,13 @@ at::Tensor paged_decode_split_indices_out(const at::Tensor &query, const at::Ten
                                           const at::Tensor &partial_sum, const at::Tensor &output,
                                           int64_t max_seq_len, int64_t split_size,
                                           std::optional<double> softmax_scale, int64_t q_len,
-                                          const std::optional<at::Tensor> &lse) {
+                                          const std::optional<at::Tensor> &lse,
+                                          const std::optional<at::Tensor> &tree_mask) {
   check_query(query);
   const int32_t kv = check_16bit_cache(query, key_cache, value_cache);
   const l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&page_indices, &page_indptr},
                                       seq_lens, partial_output, partial_max, partial_sum, output, max_seq_len,
-                                      split_size, softmax_scale, q_len, lse, kv);
+                                      split_size, softmax_scale, q_len, lse, kv, tree_mask);
   launch(query, a, false);
   return output;
 }
@@ -401,7 +414,7 @@ TORCH_LIBRARY(l20_stack, m) {
       "Tensor(c!) partial_sum, Tensor(d!) output, "
       "int max_seq_len, int split_size, "
       "float? softmax_scale=None, int q_len=1, "
-      "Tensor(e!)? lse=None) -> Tensor(d!)");
+      "Tensor(e!)? lse=None, Tensor? tree_mask=None) -> Tensor(d!)");
   m.def(
       "paged_decode_fp8_e4m3_split_out("
       "Tensor query, Tensor key_cache, Tensor value_cache, "
@@ -412,7 +425,7 @@ TORCH_LIBRARY(l20_stack, m) {
       "int max_seq_len, int split_size, "
       "float? softmax_scale=None, Tensor? k_scale_per_head=None, "
       "Tensor? v_scale_per_head=None, int q_len=1, "
-      "Tensor(e!)? lse=None) -> Tensor(d!)");
+      "Tensor(e!)? lse=None, Tensor? tree_mask=None) -> Tensor(d!)");
   m.def(
       "paged_decode_split_indices_out("
       "Tensor query, Tensor key_cache, Tensor value_cache, "
@@ -421,7 +434,7 @@ TORCH_LIBRARY(l20_stack, m) {
       "Tensor(c!) partial_sum, Tensor(d!) output, "
       "int max_seq_len, int split_size, "
       "float? softmax_scale=None, int q_len=1, "
-      "Tensor(e!)? lse=None) -> Tensor(d!)");
+      "Tensor(e!)? lse=None, Tensor? tree_mask=None) -> Tensor(d!)");
   m.def(
       "rope_and_cache(Tensor(a!)? query, Tensor(b!) key, Tensor value, Tensor positions, "
       "Tensor cos_sin_cache, bool is_neox, Tensor(c!) key_cache, Tensor(d!) value_cache, "

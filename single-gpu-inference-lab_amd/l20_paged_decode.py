@@ -57,6 +57,7 @@ def paged_decode_split_out(
     softmax_scale: Optional[float] = None,
     q_len: int = 1,
     lse: Optional[torch.Tensor] = None,
+    tree_mask: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Paged split-KV decode attention over fp16 (or bf16) caches; writes and
     returns ``output``.  The first 11 arguments are the reference's
@@ -64,7 +65,7 @@ def paged_decode_split_out(
     return torch.ops.l20_stack.paged_decode_split_out(
         query, key_cache, value_cache, block_table, seq_lens, partial_output, partial_max, partial_sum,
         output, int(max_seq_len), int(split_size), None if softmax_scale is None else float(softmax_scale),
-        int(q_len), lse,
+        int(q_len), lse, tree_mask,
     )
 
 
@@ -84,13 +85,14 @@ def paged_decode_split_indices_out(
     softmax_scale: Optional[float] = None,
     q_len: int = 1,
     lse: Optional[torch.Tensor] = None,
+    tree_mask: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """The CSR page-list variant (``l20_paged_decode.cu:600-649``): sequence b's
     pages are ``page_indices[page_indptr[b] : page_indptr[b + 1]]``."""
     return torch.ops.l20_stack.paged_decode_split_indices_out(
         query, key_cache, value_cache, page_indptr, page_indices, seq_lens, partial_output, partial_max,
         partial_sum, output, int(max_seq_len), int(split_size),
-        None if softmax_scale is None else float(softmax_scale), int(q_len), lse,
+        None if softmax_scale is None else float(softmax_scale), int(q_len), lse, tree_mask,
     )
 
 
@@ -113,6 +115,7 @@ def paged_decode_fp8_e4m3_split_out(
     v_scale_per_head: Optional[torch.Tensor] = None,
     q_len: int = 1,
     lse: Optional[torch.Tensor] = None,
+    tree_mask: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Paged FP8 e4m3fn split-KV decode attention; writes and returns ``output``.
 
@@ -138,6 +141,7 @@ def paged_decode_fp8_e4m3_split_out(
         v_scale_per_head,
         int(q_len),
         lse,
+        tree_mask,
     )
 
 
@@ -145,13 +149,13 @@ def _register_fake() -> None:
     @torch.library.register_fake("l20_stack::paged_decode_split_out")
     def _paged_decode_split_out_fake(query, key_cache, value_cache, block_table, seq_lens, partial_output,
                                      partial_max, partial_sum, output, max_seq_len, split_size,
-                                     softmax_scale=None, q_len=1, lse=None):
+                                     softmax_scale=None, q_len=1, lse=None, tree_mask=None):
         return output
 
     @torch.library.register_fake("l20_stack::paged_decode_split_indices_out")
     def _paged_decode_split_indices_out_fake(query, key_cache, value_cache, page_indptr, page_indices, seq_lens,
                                              partial_output, partial_max, partial_sum, output, max_seq_len,
-                                             split_size, softmax_scale=None, q_len=1, lse=None):
+                                             split_size, softmax_scale=None, q_len=1, lse=None, tree_mask=None):
         return output
 
     @torch.library.register_fake("l20_stack::paged_decode_fp8_e4m3_split_out")
@@ -174,6 +178,7 @@ def _register_fake() -> None:
         v_scale_per_head=None,
         q_len=1,
         lse=None,
+        tree_mask=None,
     ):
         return output
 

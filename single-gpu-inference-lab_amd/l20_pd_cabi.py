@@ -17,7 +17,7 @@ LIB_PATH = Path(__file__).with_name("libl20_paged_decode_hip.so")
 L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
 L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
 L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16 = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every extern "C" symbol declared in include/*.h.
 EXPORTED = (
@@ -63,6 +63,7 @@ class L20PdFp8Args(ctypes.Structure):
         ("batch", _i32), ("q_len", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
         ("max_seq_len", _i32), ("split_size", _i32),
         ("kv_dtype", _i32), ("page_indptr", _vp),
+        ("tree_mask", _vp), ("tree_mask_stride_batch", _i64),
     ]
 
 
@@ -153,7 +154,7 @@ def _kv_code(t) -> int:
 def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, partial_output, partial_max,
                       partial_sum, output, k_scale, v_scale, max_seq_len, split_size, *, softmax_scale=None,
                       k_scale_per_head=None, v_scale_per_head=None, q_len=1, lse=None,
-                      page_indptr=None) -> L20PdFp8Args:
+                      page_indptr=None, tree_mask=None) -> L20PdFp8Args:
     """Fill ``l20_pd_fp8_args`` from tensors (same argument order as the fp8 op).
 
     The cache dtype picks ``kv_dtype`` (fp8 e4m3fn, fp16 or bf16).  With
@@ -199,6 +200,9 @@ def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, part
     a.num_q_heads, a.head_dim = query.shape[1], query.shape[2]
     a.num_kv_heads = key_cache.shape[2]
     a.max_seq_len, a.split_size = int(max_seq_len), int(split_size)
+    if tree_mask is not None:
+        a.tree_mask = tree_mask.data_ptr()
+        a.tree_mask_stride_batch = tree_mask.stride(0) if tree_mask.dim() == 2 else 0
     return a
 
 

@@ -68,6 +68,11 @@ def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, 
     }
 
 
+def _host_tree(inp):
+    t = inp.get("tree_mask")
+    return None if t is None else t.cpu().numpy().astype(np.int64)
+
+
 def _scales(x):
     return (x, None) if isinstance(x, float) else (1.0, x)
 
@@ -100,12 +105,13 @@ def run_op(inp, split_size, *, via="torch", partial_dtype=torch.float32, with_ls
     if via == "torch":
         torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
             q, kc, vc, inp["block_table"], inp["seq_lens"], po, pm, ps, out, ks, vs,
-            inp["max_seq_len"], split_size, inp["softmax_scale"], ksph, vsph, inp["q_len"], lse)
+            inp["max_seq_len"], split_size, inp["softmax_scale"], ksph, vsph, inp["q_len"], lse,
+            inp.get("tree_mask"))
     else:
         args = cabi.args_from_tensors(
             q, kc, vc, inp["block_table"], inp["seq_lens"], po, pm, ps, out, ks, vs, inp["max_seq_len"],
             split_size, softmax_scale=inp["softmax_scale"], k_scale_per_head=ksph, v_scale_per_head=vsph,
-            q_len=inp["q_len"], lse=lse)
+            q_len=inp["q_len"], lse=lse, tree_mask=inp.get("tree_mask"))
         cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return out, lse
@@ -125,7 +131,7 @@ def run_oracle(inp, rows: Optional[Sequence[int]] = None):
         inp["block_table"].cpu().numpy(),
         inp["seq_lens"].cpu().numpy(),
         host_scale(inp["k_scale"]), host_scale(inp["v_scale"]),
-        softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows)
+        softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows, tree_mask=_host_tree(inp))
 
 
 def compare(out, lse, exp_out, exp_lse, rows: Optional[np.ndarray] = None, check_lse=True):
@@ -213,17 +219,18 @@ def run_op16(inp, split_size, *, via="torch", csr=False, partial_dtype=torch.flo
         if csr:
             torch.ops.l20_stack.paged_decode_split_indices_out(
                 q, inp["key_cache"], inp["value_cache"], inp["page_indptr"], inp["page_indices"], inp["seq_lens"],
-                po, pm, ps, out, inp["max_seq_len"], split_size, inp["softmax_scale"], inp["q_len"], lse)
+                po, pm, ps, out, inp["max_seq_len"], split_size, inp["softmax_scale"], inp["q_len"], lse,
+                inp.get("tree_mask"))
         else:
             torch.ops.l20_stack.paged_decode_split_out(
                 q, inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"], po, pm, ps, out,
-                inp["max_seq_len"], split_size, inp["softmax_scale"], inp["q_len"], lse)
+                inp["max_seq_len"], split_size, inp["softmax_scale"], inp["q_len"], lse, inp.get("tree_mask"))
     else:
         table = inp["page_indices"] if csr else inp["block_table"]
         args = cabi.args_from_tensors(
             q, inp["key_cache"], inp["value_cache"], table, inp["seq_lens"], po, pm, ps, out, 1.0, 1.0,
             inp["max_seq_len"], split_size, softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], lse=lse,
-            page_indptr=inp["page_indptr"] if csr else None)
+            page_indptr=inp["page_indptr"] if csr else None, tree_mask=inp.get("tree_mask"))
         cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return out, lse
@@ -238,4 +245,4 @@ def run_oracle16(inp, rows: Optional[Sequence[int]] = None, csr=False):
         inp["query"].float().cpu().numpy(), inp["key_cache"].float().cpu().numpy(),
         inp["value_cache"].float().cpu().numpy(), table.cpu().numpy(), inp["seq_lens"].cpu().numpy(),
         softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows,
-        page_indptr=inp["page_indptr"].cpu().numpy() if csr else None)
+        page_indptr=inp["page_indptr"].cpu().numpy() if csr else None, tree_mask=_host_tree(inp))

@@ -40,7 +40,7 @@ def test_library_exports_every_header_symbol():
     assert sorted(cabi.EXPORTED) == declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.l20_pd_abi_version() == cabi.ABI_VERSION == 2
+    assert lib.l20_pd_abi_version() == cabi.ABI_VERSION == 3
 
 
 def test_num_splits_and_default_split_size():

@@ -1,0 +1,250 @@
+"""GPU parity of speculative tree verification (ancestor bitmasks over the newest
+q_len keys) on the streaming split-KV kernel, against the CPU oracle.
+
+Visibility (``triton_tree_attention.py:1218-1240`` of the reference): draft row
+i sees the cached prefix and draft j iff ``ancestor_mask[i, j]``.  Tolerances
+are the decode parity tolerances of ``pd_helpers``.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import pd_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def random_tree(s, rng):
+    """Ancestor mask of a random tree over s drafts (parent index < child index)."""
+    parent = [-1] + [int(rng.integers(-1, i)) for i in range(1, s)]
+    m = np.zeros((s, s), dtype=bool)
+    for i in range(s):
+        j = i
+        while j >= 0:
+            m[i, j] = True
+            j = parent[j]
+    return m
+
+
+def words(mask):
+    from oracle import paged_fp8_decode_ref as ref
+
+    w = ref.tree_bits_from_mask(mask)
+    return torch.from_numpy(np.where(w >= 2**31, w - 2**32, w).astype(np.int32))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+TREE_SHAPES = [
+    # batch, hq, hkv, d, lens, q_len, split
+    (3, 8, 2, 128, [700, 37, 1500], 4, 256),     # 16 columns
+    (2, 16, 2, 128, [1000, 333], 4, 512),        # 32 columns (two 16-column tiles)
+    (2, 32, 32, 64, [530, 64], 8, 128),          # MHA, d=64
+    (2, 4, 4, 128, [900, 32], 32, 256),          # 32 drafts, group 1, one sequence all drafts
+    (4, 28, 4, 128, [2048, 17, 300, 4], 4, 512),  # Qwen-7B heads; one sequence holds only its drafts
+]
+
+
+@pytest.mark.parametrize("shape", TREE_SHAPES, ids=[f"t{i}" for i in range(len(TREE_SHAPES))])
+@pytest.mark.parametrize("via", ["torch", "cabi"])
+def test_fp8_tree_mask_matches_oracle(shape, via):
+    batch, hq, hkv, d, lens, q_len, split = shape
+    print(f"fp8 tree {shape} via={via}", flush=True)
+    rng = np.random.default_rng(len(lens) * 31 + q_len)
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, seed=7 + q_len, garbage_tail=True)
+    masks = np.stack([random_tree(q_len, rng) for _ in range(batch)])
+    inp["tree_mask"] = words(masks).cuda()
+    out, lse = H.run_op(inp, split, via=via)
+    exp_out, exp_lse = H.run_oracle(inp)
+    H.compare(out, lse, exp_out, exp_lse)
+
+
+def test_fp8_tree_shared_mask_and_arbitrary_bits():
+    """A [q_len] mask shared by the batch, with words that are not tree-shaped
+    (bit 31 set, rows seeing no draft at all)."""
+    q_len = 32
+    inp = H.make_synthetic(2, 4, 4, 128, [1200, 40], q_len=q_len, seed=3)
+    rng = np.random.default_rng(5)
+    w = rng.integers(0, 2**32, size=q_len, dtype=np.int64)
+    w[0] = 0
+    w[1] = 2**31
+    w[2] = 2**32 - 1
+    inp["tree_mask"] = torch.from_numpy(np.where(w >= 2**31, w - 2**32, w).astype(np.int32)).cuda()
+    out, lse = H.run_op(inp, 256)
+    exp_out, exp_lse = H.run_oracle(inp)
+    H.compare(out, lse, exp_out, exp_lse)
+
+
+def test_fp8_chain_tree_equals_causal():
+    """The chain mask reproduces the causal verifier bit for bit."""
+    q_len = 8
+    inp = H.make_synthetic(3, 32, 8, 128, [3000, 600, 8], q_len=q_len, seed=11)
+    base_out, base_lse = H.run_op(inp, 512)
+    chain = np.tril(np.ones((q_len, q_len), dtype=bool))
+    inp["tree_mask"] = words(chain).cuda()
+    out, lse = H.run_op(inp, 512)
+    assert torch.equal(out, base_out)
+    assert torch.equal(lse, base_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("csr", [False, True])
+def test_16bit_tree_mask_matches_oracle(dtype, csr):
+    print(f"16-bit tree dtype={dtype} csr={csr}", flush=True)
+    q_len = 6
+    rng = np.random.default_rng(17)
+    inp = H.make_synthetic16(3, 20, 4, 128, [800, 6, 2100], dtype=dtype, q_len=q_len, seed=23,
+                             garbage_tail=True, csr_pad=2 if csr else 0)
+    masks = np.stack([random_tree(q_len, rng) for _ in range(3)])
+    inp["tree_mask"] = words(masks).cuda()
+    out, lse = H.run_op16(inp, 512, csr=csr, via="cabi" if csr else "torch")
+    exp_out, exp_lse = H.run_oracle16(inp, csr=csr)
+    H.compare(out, lse, exp_out, exp_lse)
+
+
+def test_tree_mask_rejects_bad_shapes():
+    inp = H.make_synthetic(2, 8, 2, 128, [100, 50], q_len=4, seed=1)
+    inp["tree_mask"] = torch.zeros(3, 4, dtype=torch.int32, device="cuda")  # wrong batch
+    with pytest.raises(RuntimeError, match="tree_mask"):
+        H.run_op(inp, 256)
+    inp["tree_mask"] = torch.zeros(2, 4, dtype=torch.int64, device="cuda")  # wrong dtype
+    with pytest.raises(RuntimeError, match="tree_mask"):
+        H.run_op(inp, 256)
+
+
+# ------------------------------------------------------------------ Python entry points
+def _dense_oracle(query, prefix_k, prefix_v, suffix_k, suffix_v, mask, scale):
+    """fp64 attention over concat(prefix, suffix) keys: every row sees the prefix,
+    row i sees draft j iff mask[i, j] (any draft count, unlike the 32-bit words)."""
+    b, s, hq, d = query.shape
+    hkv = prefix_k.shape[2]
+    g = hq // hkv
+    p = prefix_k.shape[1]
+    visible = np.concatenate([np.ones((s, p), dtype=bool), mask], 1)  # [S, P+S]
+    out = np.zeros((b, s, hq, d))
+    for i in range(b):
+        keys = np.concatenate([prefix_k[i], suffix_k[i]], 0).astype(np.float64)
+        vals = np.concatenate([prefix_v[i], suffix_v[i]], 0).astype(np.float64)
+        q = query[i].astype(np.float64).reshape(s, hkv, g, d)
+        sc = np.einsum("ihgd,thd->ihgt", q, keys) * scale
+        sc = np.where(visible[:, None, None, :], sc, -np.inf)
+        w = np.exp(sc - sc.max(-1, keepdims=True))
+        w /= w.sum(-1, keepdims=True)
+        out[i] = np.einsum("ihgt,thd->ihgd", w, vals).reshape(s, hq, d)
+    return out
+
+
+def _paged_prefix(batch, hkv, d, cached, kv_dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    pages = (cached + 15) // 16
+    pool = batch * pages + 3
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    table = perm[: batch * pages].view(batch, pages).contiguous() if pages else torch.zeros(batch, 1, dtype=torch.int32)
+    raw_k = torch.randn(pool, 16, hkv, d, generator=g)
+    raw_v = torch.randn(pool, 16, hkv, d, generator=g)
+    if kv_dtype == "fp8":
+        import l20_pd_workloads as wl
+
+        kc, ks = wl.quantize_fp8_e4m3(raw_k.to(torch.bfloat16))
+        vc, vs = wl.quantize_fp8_e4m3(raw_v.to(torch.bfloat16))
+        from oracle import paged_fp8_decode_ref as ref
+
+        kf = ref.dequantize(kc.view(torch.uint8).numpy(), ks)
+        vf = ref.dequantize(vc.view(torch.uint8).numpy(), vs)
+    else:
+        kc, vc, ks, vs = raw_k.to(kv_dtype), raw_v.to(kv_dtype), 1.0, 1.0
+        kf, vf = kc.float().numpy(), vc.float().numpy()
+    pk = np.stack([np.concatenate([kf[p] for p in table[i].tolist()], 0)[:cached] if pages else
+                   np.zeros((0, hkv, d)) for i in range(batch)])
+    pv = np.stack([np.concatenate([vf[p] for p in table[i].tolist()], 0)[:cached] if pages else
+                   np.zeros((0, hkv, d)) for i in range(batch)])
+    return kc.cuda(), vc.cuda(), ks, vs, table.cuda(), pk, pv
+
+
+HYBRID = [
+    # batch, hq, hkv, d, cached, draft, kv
+    (2, 8, 2, 128, 1000, 4, "fp8"),
+    (2, 28, 4, 128, 2049, 8, "fp8"),      # 56 columns -> two packed chunks
+    (1, 8, 8, 128, 700, 40, torch.bfloat16),  # 40 drafts (suffix > 32) -> chunks of 32
+    (3, 16, 16, 64, 333, 5, torch.float16),
+    (2, 8, 2, 128, 0, 3, "fp8"),          # no cached prefix
+]
+
+
+@pytest.mark.parametrize("case", HYBRID, ids=[f"h{i}" for i in range(len(HYBRID))])
+def test_hybrid_tree_attention_paged_prefix(case):
+    import l20_tree_verify as tv
+
+    batch, hq, hkv, d, cached, draft, kv = case
+    print(f"hybrid {case}", flush=True)
+    qdt = torch.bfloat16 if kv in ("fp8", torch.bfloat16) else torch.float16
+    kc, vc, ks, vs, table, pk, pv = _paged_prefix(batch, hkv, d, cached, kv, seed=draft + cached)
+    g = torch.Generator().manual_seed(99 + draft)
+    query = torch.randn(batch, draft, hq, d, generator=g).to(qdt)
+    sk = torch.randn(batch, draft, hkv, d, generator=g).to(qdt)
+    sv = torch.randn(batch, draft, hkv, d, generator=g).to(qdt)
+    mask = random_tree(draft, np.random.default_rng(draft))
+    got = tv.hybrid_tree_attention_paged_prefix(
+        query.cuda(), kc, vc, sk.cuda(), sv.cuda(), table, torch.from_numpy(mask).cuda(), cached,
+        k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert got.shape == query.shape and got.dtype == qdt
+    exp = _dense_oracle(query.float().numpy(), pk, pv, sk.float().numpy(), sv.float().numpy(), mask, d ** -0.5)
+    g_np = got.float().cpu().numpy()
+    assert np.isfinite(g_np).all()
+    assert np.abs(g_np - exp).max() <= H.OUT_ATOL
+
+
+def test_causal_verifier_equals_chain_hybrid_and_paged_tree():
+    """causal_verifier_attention_paged == the hybrid path with the chain mask ==
+    the in-cache tree path over the same keys (drafts appended as the newest
+    tokens of 16-bit pages)."""
+    import l20_tree_verify as tv
+
+    batch, hq, hkv, d, cached, draft = 2, 16, 4, 128, 500, 6
+    kc, vc, _, _, table, pk, pv = _paged_prefix(batch, hkv, d, cached, torch.bfloat16, seed=4)
+    g = torch.Generator().manual_seed(5)
+    query = torch.randn(batch, draft, hq, d, generator=g).to(torch.bfloat16).cuda()
+    sk = torch.randn(batch, draft, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    sv = torch.randn(batch, draft, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    a = tv.causal_verifier_attention_paged(query, kc, vc, sk, sv, table, cached)
+    b = tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table,
+                                              tv.make_chain_tree_mask(draft, device="cuda"), cached)
+    assert torch.equal(a, b)
+    # in-cache layout: prefix + drafts in fresh pages of one cache
+    total = cached + draft
+    pages = (total + 15) // 16
+    kfull = torch.zeros(batch * pages, 16, hkv, d, dtype=torch.bfloat16)
+    vfull = torch.zeros_like(kfull)
+    full_k = np.concatenate([pk, sk.float().cpu().numpy()], 1)
+    full_v = np.concatenate([pv, sv.float().cpu().numpy()], 1)
+    for i in range(batch):
+        pad = np.zeros((pages * 16, hkv, d), dtype=np.float32)
+        pad[:total] = full_k[i]
+        kfull[i * pages:(i + 1) * pages] = torch.from_numpy(pad).view(pages, 16, hkv, d).to(torch.bfloat16)
+        pad[:] = 0
+        pad[:total] = full_v[i]
+        vfull[i * pages:(i + 1) * pages] = torch.from_numpy(pad).view(pages, 16, hkv, d).to(torch.bfloat16)
+    tbl = torch.arange(batch * pages, dtype=torch.int32).view(batch, pages).cuda()
+    lens = torch.full((batch,), total, dtype=torch.int32).cuda()
+    c = tv.paged_tree_verify_attention(query, kfull.cuda(), vfull.cuda(), tbl, lens,
+                                       tv.make_chain_tree_mask(draft, device="cuda"))
+    torch.cuda.synchronize()
+    assert c.shape == query.shape
+    assert (c.float() - a.float()).abs().max().item() <= H.OUT_ATOL
+
+
+def test_paged_tree_verify_rejects_wide_tiles():
+    import l20_tree_verify as tv
+
+    q = torch.zeros(1, 8, 32, 128, dtype=torch.bfloat16, device="cuda")  # 8 drafts x group 8 = 64 columns
+    kc = torch.zeros(4, 16, 4, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="32"):
+        tv.paged_tree_verify_attention(q, kc, kc, torch.zeros(1, 4, dtype=torch.int32, device="cuda"),
+                                       torch.full((1,), 40, dtype=torch.int32, device="cuda"),
+                                       tv.make_chain_tree_mask(8, device="cuda"))

@@ -353,3 +353,59 @@ def test_dense_kv_single_token_and_equal_keys_closed_forms():
     np.testing.assert_allclose(out[0], np.broadcast_to(v[0, :, 0].mean(0), (2, 64)), rtol=1e-5, atol=1e-6)
     s = (q[0] @ k[0, 0, 0]) / 8.0
     np.testing.assert_allclose(lse[0], s + math.log(16), rtol=1e-5)
+
+
+# ------------------------------------------------------------ tree (ancestor-mask) verify
+def test_reference_tree_attention_known_answer():
+    """The reference's KAT with its irregular ancestor mask (tests/test_tree_attention.py:36-53):
+    2 cached + 2 draft tokens, mask [[T, F], [F, T]], all-ones query, D=2."""
+    q = np.ones((2, 1, 2), np.float32)
+    k = np.array([[1, 0], [0, 1], [2, 0], [0, 2]], np.float32).reshape(4, 1, 1, 2)
+    v = np.array([[1, 0], [2, 0], [4, 0], [8, 0]], np.float32).reshape(4, 1, 1, 2)
+    kc = np.zeros((1, 16, 1, 2), np.float32)
+    vc = np.zeros_like(kc)
+    kc[0, :4], vc[0, :4] = k[:, 0], v[:, 0]
+    bits = ref.tree_bits_from_mask(np.array([[True, False], [False, True]]))
+    assert bits.tolist() == [1, 2]
+    out, _ = ref.reference_dense_kv(q, kc, vc, np.zeros((1, 1), np.int32), np.array([4]), q_len=2, tree_mask=bits)
+    s = 2 ** -0.5
+    for row, visible in enumerate(([0, 1, 2], [0, 1, 3])):
+        scores = np.array([k[t, 0, 0].sum() * s for t in visible])
+        p = np.exp(scores - scores.max())
+        p /= p.sum()
+        want = (p[:, None] * v[visible, 0, 0]).sum(0)
+        np.testing.assert_allclose(out[row, 0], want, rtol=1e-6)
+
+
+def test_chain_tree_mask_equals_causal_rule():
+    case = make_case(seed=21, batch=2, hq=4, hkv=2, d=64, lens=[21, 9], q_len=4, per_head=True)
+    chain = ref.tree_bits_from_mask(np.tril(np.ones((4, 4), bool)))
+    a = run(ref.reference, case)
+    b = run(ref.reference, case, tree_mask=chain)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_tree_reference_matches_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    q_len = 5
+    case = make_case(seed=30 + seed, batch=2, hq=4, hkv=2, d=64, lens=[37, 12], q_len=q_len)
+    # random trees: each draft token's parent is an earlier draft token (or the prefix)
+    masks = []
+    for _ in range(2):
+        anc = np.zeros((q_len, q_len), bool)
+        for i in range(q_len):
+            anc[i, i] = True
+            parent = rng.integers(-1, i) if i else -1
+            if parent >= 0:
+                anc[i] |= anc[parent]
+        masks.append(anc)
+    bits = ref.tree_bits_from_mask(np.stack(masks))
+    got = run(ref.reference, case, tree_mask=bits)
+    want = run(ref.brute_force_fp64, case, tree_mask=bits)
+    np.testing.assert_allclose(got[0], want[0], rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(got[1], want[1], rtol=2e-5, atol=2e-6)
+    # a planted mistake (bits shifted by one draft position) is caught
+    bad = run(ref.reference, case, tree_mask=bits << 1)
+    assert not np.allclose(bad[0], want[0], atol=1e-3)
