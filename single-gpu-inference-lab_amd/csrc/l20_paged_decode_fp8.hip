@@ -23,7 +23,7 @@
 //    A sequence with a single split writes the final output and LSE;
 //    otherwise the fp32 partial (O / l, m, l) goes to the caller's workspace.
 //
-//  pd_merge<QT, D>   one wave per (query row, q head), 4 per workgroup.
+//  pd_merge<QT, D, WPP>   WPP waves per (query row, q head), WPP from the split count.
 //    LSE merge of a row's splits: M = max m_s, w_s = 2^(m_s - M) l_s,
 //    out = sum w_s o_s / sum w_s, lse = ln2 (M + log2 sum w_s).
 //
@@ -1056,39 +1056,48 @@ struct MergeParams {
   int rows, num_q_heads;
 };
 
-// One wave per (query row, q head), 4 waves per workgroup.  Lane l owns
-// dims [8c, 8c + 8) of slot group g (c = l % (D/8), g = l / (D/8)), so one
-// step covers 512/D slots with 32-byte loads; the steps' loads are
-// independent, the slot groups are folded with shuffles at the end, and
-// nothing goes through LDS or a barrier.
-template <typename QT, int D>
-__global__ __launch_bounds__(256) void pd_merge(MergeParams p) {
-  constexpr int CH = D / 8;      // 8-dim chunks per row
-  constexpr int SG = 64 / CH;    // slots per step
+// WPP waves per (query row, q head) pair (WPP = 1, 2, 4, 8 or 16: enough
+// that each wave holds at most two steps of slots).  Lane l of a wave owns
+// dims [8c, 8c + 8) of slot group g (c = l % (D/8), g = l / (D/8)); wave w of
+// a pair takes slots (w + WPP * step) * G + g, G = 512/D groups, so every load
+// of a wave is independent and issued together.  Each wave folds its groups
+// with shuffles; with WPP > 1 the pair's waves then combine through LDS.
+template <typename QT, int D, int WPP>
+__global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams p) {
+  constexpr int CH = D / 8;                // 8-dim chunks per row
+  constexpr int SG = 64 / CH;              // slot groups per wave
+  constexpr int WPB = WPP > 4 ? WPP : 4;   // waves per workgroup
+  constexpr int PPB = WPB / WPP;           // pairs per workgroup
+  __shared__ float s_m[WPB], s_w[WPB];
+  __shared__ f32x4 s_acc[WPP > 1 ? WPB : 1][CH][2];
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wp = wave % WPP;
   const int c = lane % CH;
   const int g = lane / CH;
-  const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pair >= (int64_t)p.rows * p.num_q_heads) return;
-  const int row = (int)(pair / p.num_q_heads);
-  const int h = (int)(pair - (int64_t)row * p.num_q_heads);
-  const int b = row / p.q_len;
-  const int L = max(0, min(p.seq_lens[b], p.l_cap));
-  const int n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
-  if (n <= 1) return;  // the partial kernel wrote this row (or the empty row) directly
+  const int64_t pair = (int64_t)blockIdx.x * PPB + wave / WPP;
+  const bool live = pair < (int64_t)p.rows * p.num_q_heads;
+  const int row = live ? (int)(pair / p.num_q_heads) : 0;
+  const int h = live ? (int)(pair - (int64_t)row * p.num_q_heads) : 0;
+  int n = 0;
+  if (live) {
+    const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
+    n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
+  }
+  if (WPP == 1 && n <= 1) return;  // the partial kernel wrote this row (or the empty row) directly
   const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
   const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
-  // One pass, every load independent: each lane keeps an online merge
-  // (max, weight sum, weighted rows) over the slots of its group; NaN slots
-  // continue a run that started in an earlier slot and are skipped.
-  const bool final_row = pm[0] == INFINITY;  // one run wrote the whole row already
+  // Online merge (max, weight sum, weighted rows) over the lane's slots; NaN
+  // slots (a run continued from an earlier slot) never enter the sums.
+  const bool final_row = n > 1 && pm[0] == INFINITY;  // one run wrote the whole row already
   float mx = -INFINITY, wsum = 0.0f;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
-#pragma unroll 4
-  for (int s0 = 0; s0 < n; s0 += SG) {
+  const int n_here = n > 1 ? n : 0;
+#pragma unroll 2
+  for (int s0 = wp * SG; s0 < n_here; s0 += WPP * SG) {
     const int s = s0 + g;
-    if (s < n) {
+    if (s < n_here) {
       const float ms = pm[(int64_t)s * p.pm_ssplit];
       const float ls = pl[(int64_t)s * p.pl_ssplit];
       const int64_t off = base + (int64_t)s * p.po_ssplit;
@@ -1102,7 +1111,7 @@ __global__ __launch_bounds__(256) void pd_merge(MergeParams p) {
         o0 = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
         o1 = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
       }
-      if (ms == ms && ms != -INFINITY) {  // stale continuation slots never enter the sums
+      if (ms == ms && ms != -INFINITY) {
         const float m_new = fmaxf(mx, ms);
         const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
         const float w = __builtin_amdgcn_exp2f(ms - m_new) * ls;
@@ -1113,22 +1122,43 @@ __global__ __launch_bounds__(256) void pd_merge(MergeParams p) {
       }
     }
   }
-  // fold the slot groups (lane bits at and above log2(CH)): LSE-combine
-#pragma unroll
-  for (int off = CH; off < 64; off <<= 1) {
-    const float m_o = __shfl_xor(mx, off);
+  // LSE-combine (mx, wsum, acc) with another partial state.
+  auto combine = [&](float m_o, float w_o, f32x4 a0_o, f32x4 a1_o) {
     const float m_new = fmaxf(mx, m_o);
     const float ms = (m_new == -INFINITY) ? 0.0f : m_new;
     const float a = __builtin_amdgcn_exp2f(mx - ms);
     const float bo = __builtin_amdgcn_exp2f(m_o - ms);
-    const float w_o = __shfl_xor(wsum, off);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc0[e] = acc0[e] * a + __shfl_xor(acc0[e], off) * bo;
-      acc1[e] = acc1[e] * a + __shfl_xor(acc1[e], off) * bo;
-    }
+    acc0 = acc0 * a + a0_o * bo;
+    acc1 = acc1 * a + a1_o * bo;
     wsum = wsum * a + w_o * bo;
     mx = m_new;
+  };
+  // fold the slot groups (lane bits at and above log2(CH))
+#pragma unroll
+  for (int off = CH; off < 64; off <<= 1) {
+    f32x4 a0_o, a1_o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a0_o[e] = __shfl_xor(acc0[e], off);
+      a1_o[e] = __shfl_xor(acc1[e], off);
+    }
+    combine(__shfl_xor(mx, off), __shfl_xor(wsum, off), a0_o, a1_o);
+  }
+  if constexpr (WPP > 1) {
+    // fold the pair's waves: every wave publishes its state, the first folds
+    if (g == 0) {
+      s_acc[wave][c][0] = acc0;
+      s_acc[wave][c][1] = acc1;
+      if (c == 0) {
+        s_m[wave] = mx;
+        s_w[wave] = wsum;
+      }
+    }
+    __syncthreads();
+    if (wp != 0 || n <= 1) return;
+#pragma unroll
+    for (int k = 1; k < WPP; ++k)
+      combine(s_m[wave + k], s_w[wave + k], s_acc[wave + k][c][0], s_acc[wave + k][c][1]);
   }
   const float msafe = (mx == -INFINITY) ? 0.0f : mx;
   if (final_row) return;
@@ -1372,11 +1402,33 @@ hipError_t launch_partial_shape(const l20pd::PartialParams &pp, int head_dim, in
                  : launch_partial_mask<QT, KT, false>(pp, head_dim, nqt, batch, num_kv_heads, stream);
 }
 
+template <typename QT, int D, int WPP>
+hipError_t launch_merge_wpp(const l20pd::MergeParams &mp, int64_t pairs, hipStream_t stream) {
+  constexpr int WPB = WPP > 4 ? WPP : 4;
+  constexpr int PPB = WPB / WPP;
+  hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP>), dim3((unsigned)((pairs + PPB - 1) / PPB)), dim3(64 * WPB), 0,
+                     stream, mp);
+  return hipGetLastError();
+}
+
+// Waves per (row, head) pair: each wave takes at most two steps of 512/D slots.
+int merge_waves_per_pair(int num_splits, int head_dim) {
+  const int per_wave = 2 * (512 / head_dim);
+  int w = 1;
+  while (w < 16 && w * per_wave < num_splits) w <<= 1;
+  return w;
+}
+
 template <typename QT, int D>
 hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipStream_t stream) {
   const int64_t pairs = (int64_t)rows * heads;
-  hipLaunchKernelGGL((l20pd::pd_merge<QT, D>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, stream, mp);
-  return hipGetLastError();
+  switch (merge_waves_per_pair(mp.num_splits, D)) {
+    case 1: return launch_merge_wpp<QT, D, 1>(mp, pairs, stream);
+    case 2: return launch_merge_wpp<QT, D, 2>(mp, pairs, stream);
+    case 4: return launch_merge_wpp<QT, D, 4>(mp, pairs, stream);
+    case 8: return launch_merge_wpp<QT, D, 8>(mp, pairs, stream);
+    default: return launch_merge_wpp<QT, D, 16>(mp, pairs, stream);
+  }
 }
 
 // Tokens of a sequence the kernels may touch: the workspace's splits and,

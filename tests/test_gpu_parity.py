@@ -133,6 +133,17 @@ def test_fp16_partial_workspace():
     H.compare(*H.run_op(inp, 128, partial_dtype=torch.float16), *H.run_oracle(inp))
 
 
+@pytest.mark.parametrize("d,lens,split,pdt", [
+    (64, [8000, 3000, 1], 64, torch.float32),     # 125 splits: 8 waves per merged pair
+    (128, [6000, 0, 700], 64, torch.float16),     # 94 splits: 16 waves per pair, fp16 partials
+    (128, [2100, 1000], 160, torch.float32),      # 14 splits: 2 waves per pair
+])
+def test_merge_waves_per_pair(d, lens, split, pdt):
+    """The merge spreads a row's splits over 1-16 waves; every spread matches the oracle."""
+    inp = H.make_synthetic(len(lens), 16, 2, d, lens, seed=split + d)
+    H.compare(*H.run_op(inp, split, partial_dtype=pdt), *H.run_oracle(inp))
+
+
 def test_strided_kv_views_like_vllm_unbind():
     """vLLM's cache is [num_blocks, 2, 16, Hkv, D]; unbind(1) gives strided K/V views."""
     inp = H.make_synthetic(3, 16, 8, 128, [100, 1000, 37], seed=7)
