@@ -200,9 +200,18 @@ template <> __device__ __forceinline__ int pack2<_Float16>(float a, float b) {
   return __builtin_bit_cast(int, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
+// Wave-uniform reads of the call's read-only inputs (lengths, CSR offsets,
+// per-head scales) go through the constant address space, so they are scalar
+// loads counted by lgkmcnt: a vector load would be counted by vmcnt, and
+// waiting for it would also wait for every K/V block in flight.
+template <typename T> __device__ __forceinline__ T uniform_ld(const T *a, int64_t i) {
+  typedef const __attribute__((address_space(4))) T *ConstPtr;
+  return ((ConstPtr)a)[i];  // an address-space cast: C-style, as C++ casts do not convert address spaces
+}
+
 // Clamped length of sequence b (tokens past l_cap are never touched).
 __device__ __forceinline__ int clamped_len(const PartialParams &p, int b) {
-  return max(0, min(p.seq_lens[b], p.l_cap));
+  return max(0, min(uniform_ld(p.seq_lens, b), p.l_cap));
 }
 
 // Inclusive scan of one value per thread over the workgroup (<= 512 threads).
@@ -223,6 +232,16 @@ __device__ __forceinline__ int block_inclusive_scan(int v, int *s_wave) {
 }
 
 __device__ __forceinline__ int lds_uniform(const int *a, int i) { return __builtin_amdgcn_readfirstlane(a[i]); }
+
+// Relaxed workgroup-scope accesses to the LDS words that waves poll and
+// publish.  Atomic rather than volatile: the compiler keeps these as LDS
+// instructions (counted by lgkmcnt), whereas volatile LDS accesses become FLAT
+// instructions, which also count in vmcnt and so wait for every K/V load in
+// flight.
+__device__ __forceinline__ int lds_poll(int *a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void lds_put(int *a, int v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
 // Work queue of the persistent partial kernel: [0] next queue item, [1]
@@ -292,10 +311,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   constexpr bool kQPrefetch = NQT == 1;
 
   extern __shared__ int s_dyn[];  // compact mode: s_prefix[B + 1], s_len[B]
-  __shared__ volatile int s_pub[2][3];  // published item (b, s, L); b = -1: none
-  __shared__ volatile int s_seq[2];     // item number of the slot's contents
-  __shared__ int s_ack[2];              // waves other than 0 that have read the slot
-  __shared__ volatile int s_prefix_ready;
+  __shared__ int s_pub[2][3];  // published item (b, s, L); b = -1: none
+  __shared__ int s_seq[2];     // item number of the slot's contents
+  __shared__ int s_ack[2];     // waves other than 0 that have read the slot
+  __shared__ int s_prefix_ready;
 
   const int nwaves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -321,9 +340,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // Sequence b's page list and its length (a block-table row, or the CSR
   // slice; l20_paged_decode.cu:205-208).
   auto row_of = [&](int b) -> const int32_t * {
-    return p.indptr ? p.bt + p.indptr[b] : p.bt + (int64_t)b * p.bt_srow;
+    return p.indptr ? p.bt + uniform_ld(p.indptr, b) : p.bt + (int64_t)b * p.bt_srow;
   };
-  auto pages_of = [&](int b) { return p.indptr ? p.indptr[b + 1] - p.indptr[b] : p.bt_pages; };
+  auto pages_of = [&](int b) {
+    return p.indptr ? uniform_ld(p.indptr, b + 1) - uniform_ld(p.indptr, b) : p.bt_pages;
+  };
   // Page ids of split s of sequence b: lane t -> tile t (a split has <= 64
   // tiles); -1 for tiles past the split, past the page list, and for
   // out-of-range ids.
@@ -466,11 +487,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   }
 
   if (threadIdx.x == 0) {
-    s_seq[0] = -1;
-    s_seq[1] = -1;
-    s_ack[0] = nwaves - 1;  // both slots start out consumed
-    s_ack[1] = nwaves - 1;
-    s_prefix_ready = 0;
+    lds_put(&s_seq[0], -1);
+    lds_put(&s_seq[1], -1);
+    lds_put(&s_ack[0], nwaves - 1);  // both slots start out consumed
+    lds_put(&s_ack[1], nwaves - 1);
+    lds_put(&s_prefix_ready, 0);
   }
   __syncthreads();
 
@@ -574,7 +595,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     if (!more) return;
     if (!claimed) issue_claim();
     if (compact)
-      while (!__builtin_amdgcn_readfirstlane(s_prefix_ready)) __builtin_amdgcn_s_sleep(1);
+      while (!__builtin_amdgcn_readfirstlane(lds_poll(&s_prefix_ready))) __builtin_amdgcn_s_sleep(1);
     const int64_t Q = queue_total();
     for (;;) {
       const int64_t c = __builtin_amdgcn_readfirstlane(claim);
@@ -594,29 +615,28 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     const int slot = t_item & 1;
     if (wave == 0) {
       resolve();
-      while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(&s_ack[slot], __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_WORKGROUP)) < nwaves - 1)
+      while (__builtin_amdgcn_readfirstlane(lds_poll(&s_ack[slot])) < nwaves - 1)
         __builtin_amdgcn_s_sleep(1);
       if (lane == 0) {
-        __hip_atomic_store(&s_ack[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        lds_put(&s_ack[slot], 0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the reset ahead of the publication
-        s_pub[slot][0] = db;
-        s_pub[slot][1] = ds;
-        s_pub[slot][2] = dL;
-        s_seq[slot] = t_item;  // after the item fields (LDS operations of a wave execute in order)
+        lds_put(&s_pub[slot][0], db);
+        lds_put(&s_pub[slot][1], ds);
+        lds_put(&s_pub[slot][2], dL);
+        lds_put(&s_seq[slot], t_item);  // after the item fields (LDS operations of a wave execute in order)
       }
       nb = db;
       ns = ds;
       nL = dL;
       return true;
     }
-    while (__builtin_amdgcn_readfirstlane(s_seq[slot]) != t_item) {
+    while (__builtin_amdgcn_readfirstlane(lds_poll(&s_seq[slot])) != t_item) {
       if (!wait) return false;
       __builtin_amdgcn_s_sleep(1);
     }
-    nb = __builtin_amdgcn_readfirstlane(s_pub[slot][0]);
-    ns = __builtin_amdgcn_readfirstlane(s_pub[slot][1]);
-    nL = __builtin_amdgcn_readfirstlane(s_pub[slot][2]);
+    nb = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][0]));
+    ns = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][1]));
+    nL = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][2]));
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // acknowledge only after the reads
     if (lane == 0) __hip_atomic_fetch_add(&s_ack[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return true;
@@ -625,7 +645,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   if (compact && wave == nwaves - 1) {
     build_prefix();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the flag follows the table (LDS operations of a wave execute in order)
-    if (lane == 0) s_prefix_ready = 1;
+    if (lane == 0) lds_put(&s_prefix_ready, 1);
   }
 
   int hh = 0;
@@ -696,8 +716,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       }
       if (n_ready) set_next();
 
-      const float k_scale = p.k_scale_ph ? p.k_scale_ph[kvh] : p.k_scale;
-      const float v_scale = p.v_scale_ph ? p.v_scale_ph[kvh] : p.v_scale;
+      const float k_scale = p.k_scale_ph ? uniform_ld(p.k_scale_ph, kvh) : p.k_scale;
+      const float v_scale = p.v_scale_ph ? uniform_ld(p.v_scale_ph, kvh) : p.v_scale;
       const float c_log2 = k_scale * p.qk_scale_log2;
       // ---- masking: keys before draft0 are visible to every column; key
       // draft0 + j to draft row i when j <= i (causal) or when bit j of the
@@ -1411,9 +1431,11 @@ hipError_t launch_merge_wpp(const l20pd::MergeParams &mp, int64_t pairs, hipStre
   return hipGetLastError();
 }
 
-// Waves per (row, head) pair: each wave takes at most two steps of 512/D slots.
+// Waves per (row, head) pair: each wave takes at most four steps of 512/D
+// slots (a second wave costs more than it saves below that: config 3 with 16
+// slots merged in 6.4 us on two waves per pair, 5.3 us on one).
 int merge_waves_per_pair(int num_splits, int head_dim) {
-  const int per_wave = 2 * (512 / head_dim);
+  const int per_wave = 4 * (512 / head_dim);
   int w = 1;
   while (w < 16 && w * per_wave < num_splits) w <<= 1;
   return w;
