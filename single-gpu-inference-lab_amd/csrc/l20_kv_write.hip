@@ -1,7 +1,16 @@
 // Paged KV-cache producer for MI355X (gfx950): rotary embedding of Q and K
 // and the paged write of K and V into fp8 (OCP e4m3fn) or 16-bit caches.
 //
-//  kv_rope_write<T, CT>   grid (num_tokens, ceil(max(Hq, Hkv) / 4)), 4 waves.
+//  kv_rope_write8<T, CT, CS>   the fast path: every Q and K head row of the
+//    call is one row of the work; a lane owns eight contiguous dims (16-byte
+//    loads and stores), D/8 lanes a row, and each lane takes two rows with
+//    all their loads issued before any arithmetic.  A neox pair partner lies
+//    half/8 lanes away in the same row and is exchanged with a lane shuffle;
+//    cos and sin arrive as 8 (neox) or 4 (interleaved) consecutive values.
+//    Taken when rows, caches and the cos/sin table are 16-byte aligned,
+//    head_dim % 8 == 0 and, for neox, rotary_dim % 16 == 0.
+//
+//  kv_rope_write<T, CT>   the general path: grid (num_tokens, ceil(max(Hq, Hkv) / 4)), 4 waves.
 //    Wave w of workgroup (t, g) owns head h = 4 g + w of token t; lane l owns
 //    the four contiguous dims [4 l, 4 l + 4) (head_dim <= 256).  A neox pair
 //    partner lies rotary_dim / 2 dims away (another lane's four dims, loaded
@@ -28,6 +37,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "l20_kv_write.h"
 
@@ -40,6 +50,8 @@ void clear_error();
 namespace l20kv {
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -141,6 +153,44 @@ __device__ __forceinline__ void rope4(const Params &p, const T *row, int64_t pos
   }
 }
 
+// ---- fast path helpers: eight consecutive elements of T as one 16-byte word ----
+template <typename T> __device__ __forceinline__ void unpack8(i32x4 w, float (&x)[8]) {
+  const T *e = reinterpret_cast<const T *>(&w);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = to_f32(e[i]);
+}
+template <typename T> __device__ __forceinline__ i32x4 pack8(const float (&x)[8]) {
+  const float lo[4] = {x[0], x[1], x[2], x[3]};
+  const float hi[4] = {x[4], x[5], x[6], x[7]};
+  const i32x2 a = pack4<T>(lo), b = pack4<T>(hi);
+  return i32x4{a[0], a[1], b[0], b[1]};
+}
+// n (4 or 8) consecutive cos/sin values from a table of CS type (0 bf16, 1 fp16, 2 fp32).
+template <int CS, int N> __device__ __forceinline__ void load_cs(const void *base, int64_t off, float (&c)[8]) {
+  if constexpr (CS == 2) {
+    const float *src = reinterpret_cast<const float *>(base) + off;
+    const f32x4 a = *reinterpret_cast<const f32x4 *>(src);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = a[i];
+    if constexpr (N == 8) {
+      const f32x4 b = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[4 + i] = b[i];
+    }
+  } else {
+    typedef typename std::conditional<CS == 0, __bf16, _Float16>::type E;
+    const E *src = reinterpret_cast<const E *>(base) + off;
+    if constexpr (N == 8) {
+      unpack8<E>(*reinterpret_cast<const i32x4 *>(src), c);
+    } else {
+      float q[4];
+      load4(src, q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = q[i];
+    }
+  }
+}
+
 // Four values -> four e4m3fn codes in one dword: RNE of clamp(x / scale).
 __device__ __forceinline__ int quant4(const float (&x)[4], float scale) {
   float y[4];
@@ -149,6 +199,137 @@ __device__ __forceinline__ int quant4(const float (&x)[4], float scale) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
   return w;
+}
+
+constexpr int kRowsPerLane = 2;
+
+// Rows [0, rows_q) are Q head rows (token r / Hq, head r % Hq), the next
+// rows_k are K head rows (token r / Hkv): rotated in place, and for K also the
+// K and V cache writes.  Four waves; a lane group of lpr = D/8 lanes per row.
+template <typename T, int CT, int CS>
+__global__ __launch_bounds__(256) void kv_rope_write8(Params p, int64_t rows_q, int64_t rows_all) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lpr = p.d >> 3;     // lanes per row
+  const int rpw = 64 / lpr;     // rows per wave and pass
+  const int g = lane / lpr;
+  const int l = lane - g * lpr;
+  const int e0 = 8 * l;
+  const int half = p.rot >> 1;
+  const bool rot_lane = e0 < p.rot;
+  const int64_t first = (int64_t)blockIdx.x * (4 * rpw * kRowsPerLane);
+
+  // ---- loads of all of this lane's rows ----
+  i32x4 xw[kRowsPerLane], vw[kRowsPerLane];
+  int64_t pos[kRowsPerLane], slot[kRowsPerLane];
+  float ksc[kRowsPerLane], vsc[kRowsPerLane];  // the K row's cache scales (loaded with the row)
+  T *row[kRowsPerLane];
+  int head[kRowsPerLane];
+  bool live[kRowsPerLane], is_k[kRowsPerLane];
+#pragma unroll
+  for (int u = 0; u < kRowsPerLane; ++u) {
+    const int64_t r = first + (int64_t)(u * 4 + wave) * rpw + g;
+    live[u] = g < rpw && r < rows_all;
+    is_k[u] = r >= rows_q;
+    int64_t t = 0;
+    int h = 0;
+    if (live[u]) {
+      if (!is_k[u]) {
+        t = r / p.hq;
+        h = (int)(r - t * p.hq);
+        row[u] = reinterpret_cast<T *>(p.q) + t * p.q_st + (int64_t)h * p.q_sh;
+      } else {
+        const int64_t rk = r - rows_q;
+        t = rk / p.hkv;
+        h = (int)(rk - t * p.hkv);
+        row[u] = reinterpret_cast<T *>(p.k) + t * p.k_st + (int64_t)h * p.k_sh;
+        vw[u] = *reinterpret_cast<const i32x4 *>(reinterpret_cast<const T *>(p.v) + t * p.v_st +
+                                                 (int64_t)h * p.v_sh + e0);
+        slot[u] = p.slots[t];
+        if constexpr (CT == 0) {
+          ksc[u] = p.k_scale_ph ? p.k_scale_ph[h] : p.k_scale;
+          vsc[u] = p.v_scale_ph ? p.v_scale_ph[h] : p.v_scale;
+        }
+      }
+      xw[u] = *reinterpret_cast<const i32x4 *>(row[u] + e0);
+      pos[u] = p.pos[t];
+    }
+    head[u] = h;
+  }
+  // ---- cos / sin of the lanes' dims ----
+  float c[kRowsPerLane][8], sn[kRowsPerLane][8];
+#pragma unroll
+  for (int u = 0; u < kRowsPerLane; ++u) {
+    if (live[u] && rot_lane) {
+      const int64_t base = pos[u] * p.cs_sp;
+      if (p.neox) {
+        const int t0 = e0 < half ? e0 : e0 - half;
+        load_cs<CS, 8>(p.cs, base + t0, c[u]);
+        load_cs<CS, 8>(p.cs, base + half + t0, sn[u]);
+      } else {
+        load_cs<CS, 4>(p.cs, base + (e0 >> 1), c[u]);
+        load_cs<CS, 4>(p.cs, base + half + (e0 >> 1), sn[u]);
+      }
+    }
+  }
+  // ---- rotate, store back, write the caches ----
+#pragma unroll
+  for (int u = 0; u < kRowsPerLane; ++u) {
+    // the neox partner's words, from the lane half/8 away in the same row (every lane shuffles)
+    const int src = g * lpr + (e0 < half ? l + (half >> 3) : l - (half >> 3));
+    i32x4 pw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pw[i] = __shfl(xw[u][i], (p.neox && rot_lane) ? src : lane);
+    if (!live[u]) continue;
+    float x[8];
+    unpack8<T>(xw[u], x);
+    if (rot_lane) {
+      float y[8];
+      if (p.neox) {
+        float pr[8];
+        unpack8<T>(pw, pr);
+        const float sg = e0 < half ? -1.0f : 1.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float a = x[i] * c[u][i];
+          const float b = (pr[i] * sn[u][i]) * sg;
+          y[i] = a + b;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float a = x[i] * c[u][i >> 1];
+          const float b = (x[i ^ 1] * sn[u][i >> 1]) * ((i & 1) ? 1.0f : -1.0f);
+          y[i] = a + b;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = y[i];
+    }
+    const i32x4 out = pack8<T>(x);
+    *reinterpret_cast<i32x4 *>(row[u] + e0) = out;
+    if (!is_k[u]) continue;
+    const int64_t sl = slot[u];
+    const int64_t page = sl >> 4;
+    if (sl < 0 || page >= p.num_pages) continue;  // not stored
+    const int h = head[u];
+    const int64_t ko = page * p.kc_sp + (sl & 15) * p.kc_st + (int64_t)h * p.kc_sh + e0;
+    const int64_t vo = page * p.vc_sp + (sl & 15) * p.vc_st + (int64_t)h * p.vc_sh + e0;
+    if constexpr (CT == 0) {
+      float kv[8], v[8];
+      unpack8<T>(out, kv);  // quantise the stored model-dtype values
+      unpack8<T>(vw[u], v);
+      const float ks = ksc[u], vs = vsc[u];
+      const float k_lo[4] = {kv[0], kv[1], kv[2], kv[3]}, k_hi[4] = {kv[4], kv[5], kv[6], kv[7]};
+      const float v_lo[4] = {v[0], v[1], v[2], v[3]}, v_hi[4] = {v[4], v[5], v[6], v[7]};
+      *reinterpret_cast<i32x2 *>(reinterpret_cast<uint8_t *>(p.kc) + ko) = i32x2{quant4(k_lo, ks), quant4(k_hi, ks)};
+      *reinterpret_cast<i32x2 *>(reinterpret_cast<uint8_t *>(p.vc) + vo) = i32x2{quant4(v_lo, vs), quant4(v_hi, vs)};
+    } else {
+      *reinterpret_cast<i32x4 *>(reinterpret_cast<T *>(p.kc) + ko) = out;
+      *reinterpret_cast<i32x4 *>(reinterpret_cast<T *>(p.vc) + vo) = vw[u];
+    }
+  }
 }
 
 template <typename T, int CT>
@@ -325,6 +506,46 @@ l20kv::Params params(const l20_pd_kv_write_args &a) {
   return p;
 }
 
+// The fast path's layout requirements (16-byte rows and cache chunks, lane-aligned neox halves).
+bool fast_path_ok(const l20_pd_kv_write_args &a) {
+  if (a.head_dim % 8 || (a.is_neox && a.rotary_dim % 16)) return false;
+  const uint64_t qkv = (uint64_t)(uintptr_t)a.key | (uint64_t)(uintptr_t)a.value |
+                       (uint64_t)(a.k_stride_token * 2) | (uint64_t)(a.k_stride_head * 2) |
+                       (uint64_t)(a.v_stride_token * 2) | (uint64_t)(a.v_stride_head * 2) |
+                       (a.query ? ((uint64_t)(uintptr_t)a.query | (uint64_t)(a.q_stride_token * 2) |
+                                   (uint64_t)(a.q_stride_head * 2))
+                                : 0);
+  if (qkv % 16) return false;
+  const bool fp8 = a.cache_dtype == L20_PD_KV_FP8_E4M3;
+  const int64_t es = fp8 ? 1 : 2;
+  const uint64_t cb = (uint64_t)(uintptr_t)a.key_cache | (uint64_t)(uintptr_t)a.value_cache |
+                      (uint64_t)(a.kc_stride_page * es) | (uint64_t)(a.kc_stride_token * es) |
+                      (uint64_t)(a.kc_stride_head * es) | (uint64_t)(a.vc_stride_page * es) |
+                      (uint64_t)(a.vc_stride_token * es) | (uint64_t)(a.vc_stride_head * es);
+  if (cb % (uint64_t)(8 * es)) return false;
+  if (a.rotary_dim > 0) {
+    const int64_t cs_es = a.cs_dtype == L20_PD_FP32 ? 4 : 2;
+    const uint64_t cs = (uint64_t)(uintptr_t)a.cos_sin_cache | (uint64_t)(a.cs_stride_position * cs_es) |
+                        (uint64_t)(a.rotary_dim / 2 * cs_es);
+    // neox: 8 values per 16-byte load; interleaved: 4 values (8 bytes, or 16 for fp32)
+    if (cs % (uint64_t)(a.is_neox ? 16 : 4 * cs_es)) return false;
+  }
+  return true;
+}
+
+template <typename T, int CT>
+void launch_fast(const l20kv::Params &p, int cs_dtype, int64_t rows_q, int64_t rows_all, hipStream_t s) {
+  const int lpr = p.d / 8;
+  const int64_t rows_per_wg = (int64_t)4 * (64 / lpr) * l20kv::kRowsPerLane;
+  const dim3 grid((unsigned)((rows_all + rows_per_wg - 1) / rows_per_wg));
+  if (cs_dtype == 2)
+    hipLaunchKernelGGL((l20kv::kv_rope_write8<T, CT, 2>), grid, dim3(256), 0, s, p, rows_q, rows_all);
+  else if (cs_dtype == 1)
+    hipLaunchKernelGGL((l20kv::kv_rope_write8<T, CT, 1>), grid, dim3(256), 0, s, p, rows_q, rows_all);
+  else
+    hipLaunchKernelGGL((l20kv::kv_rope_write8<T, CT, 0>), grid, dim3(256), 0, s, p, rows_q, rows_all);
+}
+
 int32_t launched() {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -349,10 +570,23 @@ int32_t l20_pd_rope_and_cache(const l20_pd_kv_write_args *a, void *stream) {
   const int32_t rc = check(a);
   if (rc != L20_PD_OK || a->num_tokens == 0) return rc;
   const l20kv::Params p = params(*a);
-  const int heads = std::max(p.hq, p.hkv);
-  const dim3 grid((unsigned)a->num_tokens, (unsigned)((heads + 3) / 4));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool bf = a->dtype == L20_PD_BF16;
+  if (fast_path_ok(*a)) {
+    const int64_t rows_q = (int64_t)a->num_tokens * p.hq;
+    const int64_t rows_all = rows_q + (int64_t)a->num_tokens * p.hkv;
+    const bool fp8 = a->cache_dtype == L20_PD_KV_FP8_E4M3;
+    if (bf) {
+      if (fp8) launch_fast<__bf16, 0>(p, p.cs_dtype, rows_q, rows_all, s);
+      else launch_fast<__bf16, 1>(p, p.cs_dtype, rows_q, rows_all, s);
+    } else {
+      if (fp8) launch_fast<_Float16, 0>(p, p.cs_dtype, rows_q, rows_all, s);
+      else launch_fast<_Float16, 1>(p, p.cs_dtype, rows_q, rows_all, s);
+    }
+    return launched();
+  }
+  const int heads = std::max(p.hq, p.hkv);
+  const dim3 grid((unsigned)a->num_tokens, (unsigned)((heads + 3) / 4));
   if (a->cache_dtype == L20_PD_KV_FP8_E4M3) {
     if (bf)
       hipLaunchKernelGGL((l20kv::kv_rope_write<__bf16, 0>), grid, dim3(256), 0, s, p);

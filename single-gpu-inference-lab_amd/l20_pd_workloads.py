@@ -113,13 +113,16 @@ def _gen(device: Union[str, torch.device], seed: int) -> torch.Generator:
 
 
 def make_inputs(cfg: DecodeConfig, device: Union[str, torch.device] = "cpu",
-                seed: Optional[int] = None, chunk_pages: int = 4096) -> dict:
+                seed: Optional[int] = None, chunk_pages: int = 4096,
+                kv_dtype: Optional[torch.dtype] = None) -> dict:
     """Build one seeded input set for ``cfg`` on ``device``.
 
     Returns a dict with ``query`` [B*q, Hq, D] bf16, ``key_cache`` /
     ``value_cache`` [P, 16, Hkv, D] float8_e4m3fn, ``block_table`` [B, max_pages]
     int32, ``seq_lens`` [B] int32, ``k_scale`` / ``v_scale`` (float or fp32
-    [Hkv]), ``softmax_scale``, ``q_len`` and ``max_seq_len``.
+    [Hkv]), ``softmax_scale``, ``q_len`` and ``max_seq_len``.  With
+    ``kv_dtype`` bf16 (or fp16) the caches keep that dtype (the query takes it
+    too) and both scales are 1.0.
     """
     seed = cfg.seed if seed is None else seed
     cpu = _gen("cpu", seed)
@@ -144,17 +147,21 @@ def make_inputs(cfg: DecodeConfig, device: Union[str, torch.device] = "cpu",
     dev = torch.device(device)
     g = _gen(dev, seed + 1)
     rows = cfg.batch * cfg.q_len
+    q_dtype = kv_dtype if kv_dtype is not None else torch.bfloat16
     query = torch.randn(rows, cfg.num_q_heads, cfg.head_dim, generator=g, device=dev,
-                        dtype=torch.float32).to(torch.bfloat16)
+                        dtype=torch.float32).to(q_dtype)
     shape = (pool, PAGE_SIZE, cfg.num_kv_heads, cfg.head_dim)
     caches = []
     for _ in range(2):
         # Generate in page chunks so that the fp32 staging stays bounded.
-        raw = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+        raw = torch.empty(shape, dtype=q_dtype, device=dev)
         for start in range(0, pool, chunk_pages):
             stop = min(start + chunk_pages, pool)
             raw[start:stop] = torch.randn((stop - start,) + shape[1:], generator=g, device=dev,
-                                          dtype=torch.float32).to(torch.bfloat16)
+                                          dtype=torch.float32).to(q_dtype)
+        if kv_dtype is not None:
+            caches.append((raw, 1.0))
+            continue
         codes, scale = quantize_fp8_e4m3(raw, per_head_axis=2 if cfg.per_head_scales else None)
         del raw
         caches.append((codes, scale))
@@ -175,6 +182,7 @@ def make_inputs(cfg: DecodeConfig, device: Union[str, torch.device] = "cpu",
     }
 
 
-def kv_bytes(seq_lens: torch.Tensor, num_kv_heads: int, head_dim: int) -> int:
-    """Algorithmic FP8 K+V bytes read per call: ``sum(L) * Hkv * D * 2``."""
-    return int(seq_lens.to(torch.int64).sum()) * num_kv_heads * head_dim * 2
+def kv_bytes(seq_lens: torch.Tensor, num_kv_heads: int, head_dim: int, elem_bytes: int = 1) -> int:
+    """Algorithmic K+V bytes read per call: ``sum(L) * Hkv * D * 2 * elem_bytes``
+    (1 for fp8 caches, 2 for 16-bit ones)."""
+    return int(seq_lens.to(torch.int64).sum()) * num_kv_heads * head_dim * 2 * elem_bytes

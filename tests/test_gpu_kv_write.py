@@ -112,6 +112,9 @@ ROPE = [
     (20, 4, 4, 128, 64, True),
     (33, 16, 8, 64, 32, False),
     (5, 32, 8, 256, 256, True),
+    (19, 6, 3, 96, 96, True),     # 12 lanes a row: 5 rows a wave, 4 idle lanes
+    (21, 4, 2, 36, 24, False),    # head_dim % 8 != 0: the general path
+    (15, 4, 2, 32, 24, True),     # neox halves not lane-aligned: the general path
 ]
 
 
@@ -156,6 +159,36 @@ def test_rope_and_cache_bit_exact(spec, dtype, cs_dtype, cache):
     else:
         np.testing.assert_array_equal(_np(kc), want_kc)
         np.testing.assert_array_equal(_np(vc), want_vc)
+
+
+def test_rope_and_cache_rows_only_8_byte_aligned():
+    """Q/K/V rows 8-byte but not 16-byte aligned (views at an offset of four
+    elements) take the general path and give the same bytes."""
+    from oracle import kv_write_ref as kw
+    import l20_rope_kv
+
+    T, hq, hkv, d = 23, 8, 2, 64
+    c = _case(T, hq, hkv, d, 64, torch.bfloat16, torch.bfloat16, seed=5)
+    def offset_view(x):
+        big = torch.zeros(x.shape[0], x.shape[1], d + 4, dtype=x.dtype)
+        big[..., 4:] = x
+        return big.cuda()[..., 4:]
+    q, k, v = offset_view(c["q"]), offset_view(c["k"]), offset_view(c["v"])
+    assert q.data_ptr() % 16 == 8
+    kc = torch.zeros(c["pages"], 16, hkv, d, dtype=torch.float8_e4m3fn).cuda()
+    vc = torch.zeros_like(kc)
+    q_in, k_in, v_in = _np(q), _np(k), _np(v)
+    l20_rope_kv.l20_rope_and_cache(q, k, v, c["pos"].cuda(), c["cs"].cuda(), True, kc, vc, c["slots"].cuda(),
+                                   k_scale=0.03, v_scale=0.02)
+    torch.cuda.synchronize()
+    kc0 = np.zeros(kc.shape, np.uint8)
+    want_q, want_k, want_kc, want_vc = kw.rope_and_cache(
+        q_in, k_in, v_in, c["pos"].numpy(), _np(c["cs"]), True, kc0, kc0.copy(), c["slots"].numpy(),
+        dtype="bf16", cache_fp8=True, k_scale=0.03, v_scale=0.02)
+    np.testing.assert_array_equal(_np(q), want_q)
+    np.testing.assert_array_equal(_np(k), want_k)
+    np.testing.assert_array_equal(kc.view(torch.uint8).cpu().numpy(), want_kc)
+    np.testing.assert_array_equal(vc.view(torch.uint8).cpu().numpy(), want_vc)
 
 
 @pytest.mark.parametrize("per_head", [True, False])
