@@ -173,7 +173,9 @@ int32_t l20_pd_fp8_e4m3_merge(const l20_pd_fp8_args *args, void *stream);
 
 /* Split size the library picks for a call shape when the caller has no
  * preference: a power of two in [64, 1024] -- 1024 above 32768 tokens, else
- * 512, halved while a max_seq_len sequence would have fewer than ~8 splits.
+ * 512, halved while a max_seq_len sequence would have fewer than ~8 splits,
+ * then doubled while that lets batch x splits items fit one round of the
+ * persistent grid (cu_count x 8 waves / waves per workgroup).
  * (The reference hook passes a fixed 512, install_l20_fp8_paged_decode.py.) */
 int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads,
                                   int32_t max_seq_len, int32_t cu_count);
@@ -188,9 +190,10 @@ int32_t l20_pd_fp8_e4m3_dequant_bf16(const uint8_t *src, uint16_t *dst,
                                      int64_t n, void *stream);
 
 /* HBM calibration (no reference counterpart; measurement support).
- * stream_read reads `bytes` once with 16-byte nontemporal loads over
- * `blocks` workgroups of 256 threads (sink: int32 [blocks], practically never
- * written); stream_copy copies `bytes` from src to dst.  Used to measure the
+ * stream_read reads `bytes` once: workgroup i of `blocks` (256 threads)
+ * reads the i-th contiguous chunk of ceil(bytes / blocks) bytes, rounded up
+ * to 4 KiB, with 16-byte buffer loads (sink: int32 [blocks], practically
+ * never written); stream_copy copies `bytes` from src to dst.  Used to measure the
  * device's read ceiling and to scale FETCH_SIZE / WRITE_SIZE counters. */
 int32_t l20_pd_stream_read(const void *src, int64_t bytes, int32_t *sink,
                            int32_t blocks, void *stream);

@@ -1242,21 +1242,27 @@ __global__ void dequant_bf16_kernel(const uint8_t *src, uint16_t *dst, int64_t n
 // HBM calibration kernels: a pure streaming read and a plain copy, used to
 // measure the read ceiling of the device and to scale FETCH_SIZE/WRITE_SIZE.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void stream_read_kernel(const i32x4 *src, int64_t n16, int *sink) {
+// Workgroup i reads the i-th contiguous chunk of `chunk` bytes through a
+// buffer resource, 16 loads of 16 bytes per lane in flight (contiguous
+// chunks stream faster than a grid-stride walk: 6.2-6.3 vs 5.5-6.0 TB/s on
+// MI355X over 1 GiB buffers).  Loads past the chunk return zero (range check).
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t *src, int64_t nbytes, int64_t chunk,
+                                                         int *sink) {
+  constexpr int U = 16;
+  constexpr int kStep = 256 * 16;  // bytes one load instruction of the workgroup covers
+  const int64_t base = (int64_t)blockIdx.x * chunk;
+  if (base >= nbytes) return;
+  const int len = (int)(nbytes - base < chunk ? nbytes - base : chunk);
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src) + base, (short)0, len, kBufferWord3);
   int acc = 0;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + 3 * stride < n16; i += 4 * stride) {
-    const i32x4 a = __builtin_nontemporal_load(src + i);
-    const i32x4 b = __builtin_nontemporal_load(src + i + stride);
-    const i32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
-    const i32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
-    acc ^= a[0] ^ a[1] ^ a[2] ^ a[3] ^ b[0] ^ b[1] ^ b[2] ^ b[3] ^ c[0] ^ c[1] ^ c[2] ^ c[3] ^ d[0] ^ d[1] ^ d[2] ^
-           d[3];
-  }
-  for (; i < n16; i += stride) {
-    const i32x4 a = src[i];
-    acc ^= a[0] ^ a[1] ^ a[2] ^ a[3];
+  for (int off = (int)threadIdx.x * 16; off < len; off += U * kStep) {
+    i32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      v[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + u * kStep, 0, 0));
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
   }
   if (acc == 0x7fffffff) sink[blockIdx.x] = acc;  // keeps the loads live; practically never stores
 }
@@ -1634,14 +1640,21 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
   // Measured on MI355X over the benchmark workloads: 512-token splits (the
   // reference hook's default) for ragged serving batches, 1024 for long
   // contexts (fewer partials to merge), and at least ~8 splits per sequence
-  // for short contexts, where the launch is latency-bound.  The batch, head
-  // and CU counts are part of the signature for future heuristics.
-  (void)batch;
-  (void)num_kv_heads;
-  (void)cu_count;
+  // for short contexts, where the launch is latency-bound.
   if (max_seq_len > 32768) return 1024;
   int32_t s = 512;
   while (s > 64 && (int64_t)s * 8 > max_seq_len) s >>= 1;
+  // Double the split while that lets every (sequence, split) item of a batch
+  // at max_seq_len start in the first round of the persistent grid (one item
+  // per workgroup: no item transition, which costs a query reload in the
+  // two-tile kernel).  Grid estimate: CUs x 8 waves (2 per SIMD at the
+  // kernel's occupancy) / waves per workgroup.  Verify shape (64 x 4096,
+  // 8 KV heads): 512 -> 1024, 142 -> 126 us per partial launch.
+  const int64_t grid = (int64_t)(cu_count > 0 ? cu_count : 256) *
+                       std::max(1, 8 / partial_waves(num_kv_heads > 0 ? num_kv_heads : 1));
+  while (s < 1024 && (int64_t)batch * l20_pd_num_splits(max_seq_len, s) > grid &&
+         (int64_t)batch * l20_pd_num_splits(max_seq_len, 2 * s) <= grid)
+    s <<= 1;
   return s;
 }
 
@@ -1691,8 +1704,11 @@ int32_t l20_pd_stream_read(const void *src, int64_t bytes, int32_t *sink, int32_
   g_last_error[0] = '\0';
   if (!src || !sink || bytes < 0 || bytes % 16 || ((uintptr_t)src % 16) || blocks <= 0)
     return fail(L20_PD_EINVAL, "stream_read needs a 16-byte aligned buffer, a multiple of 16 bytes and blocks > 0");
+  // chunks of whole 4 KiB units, each below 2 GiB (the buffer range)
+  const int64_t chunk = ((bytes + blocks - 1) / blocks + 4095) / 4096 * 4096;
+  if (chunk >= ((int64_t)1 << 31)) return fail(L20_PD_EINVAL, "stream_read: more blocks needed (chunk >= 2 GiB)");
   hipLaunchKernelGGL(l20pd::stream_read_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
-                     reinterpret_cast<const l20pd::i32x4 *>(src), bytes / 16, sink);
+                     reinterpret_cast<const uint8_t *>(src), bytes, chunk, sink);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));

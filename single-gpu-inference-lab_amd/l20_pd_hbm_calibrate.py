@@ -29,8 +29,8 @@ if str(HERE) not in sys.path:
 
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--bytes", type=int, default=256 * 2**20)
-    ap.add_argument("--buffers", type=int, default=5)
+    ap.add_argument("--bytes", type=int, default=2**30)
+    ap.add_argument("--buffers", type=int, default=3)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--blocks", type=int, default=4096)
     args = ap.parse_args()

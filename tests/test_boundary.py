@@ -57,6 +57,11 @@ def test_num_splits_and_default_split_size():
     assert lib.l20_pd_default_split_size(128, 4, 8192, 256) == 512
     assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 256
     assert lib.l20_pd_default_split_size(4, 2, 512, 256) == 64
+    # doubled when that fits every item in one round of the persistent grid
+    # (64 sequences x 4 splits on 256 one-workgroup CUs), never past 1024
+    assert lib.l20_pd_default_split_size(64, 8, 4096, 256) == 1024
+    assert lib.l20_pd_default_split_size(64, 8, 4096, 128) == 512
+    assert lib.l20_pd_default_split_size(8, 8, 32768, 256) == 1024
 
 
 def valid_args():
