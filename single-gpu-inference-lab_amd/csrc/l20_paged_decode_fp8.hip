@@ -2,12 +2,12 @@
 //
 // Two kernels per call, both enqueued on the caller's stream:
 //
-//  pd_fp8_partial<QT, KT, D, NQT, TREE>  persistent: CUs x occupancy workgroups, one
+//  pd_fp8_partial<QT, KT, D, NQT, TREE, NB>  persistent: CUs x occupancy workgroups, one
 //    wave per KV head (W waves, W the largest divisor of Hkv up to 8).
 //    A work item is one (sequence, split) pair; every wave of the workgroup
 //    computes attention for ALL query rows of its KV head (GQA group x
 //    q_len, padded to 16 * NQT MFMA columns), so each K/V page is read from
-//    HBM exactly once.  Each wave streams 32-token blocks through two
+//    HBM exactly once.  Each wave streams 32-token blocks through NB (1 or 2)
 //    register buffers without draining between items (the next item's page
 //    ids, query and first blocks load while the current one finishes).
 //    Per block and lane:
@@ -59,9 +59,13 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr int kPage = 16;
 constexpr int kMaxWaves = 8;       // waves per partial workgroup (one per KV head)
 constexpr int kMaxCompactBatch = 4096;  // sequences whose work list fits in LDS
-constexpr int kClaimLead = 9;    // blocks before a unit's end at which its successor is claimed
-constexpr int kPublishLead = 6;  // ... published by wave 0 and first polled by the other waves
-constexpr int kNeedLead = 3;     // ... at the latest picked up (its first block loads two blocks later)
+// Hand-off leads, in blocks before a unit's end, for a stream of NB blocks in
+// flight: the successor is needed NB + 1 blocks before the end (its first
+// block is the refill after the next step), published 3 blocks earlier and
+// claimed 3 blocks before that.
+constexpr int need_lead(int nb) { return nb + 1; }
+constexpr int publish_lead(int nb) { return nb + 4; }
+constexpr int claim_lead(int nb) { return nb + 7; }
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: dword 3 (format bits)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -277,18 +281,19 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // published to all waves early enough for the tail of the item to stream its
 // first blocks.
 //
-// Block stream.  A wave keeps two 32-token blocks of raw fp8 K/V in
-// registers.  After computing block k of unit U it refills that buffer with
-// stream position k + 2: U's own block, or one of the first two blocks of
-// the next unit N, whose page ids (and, for one query tile, query operand)
-// are loaded a few blocks before U ends.  The stream never drains between units; block
-// k of a unit sits in buffer (k + par) & 1, par carried over from unit to
-// unit.
+// Block stream.  A wave keeps NB 32-token blocks of raw fp8 K/V in registers
+// (two; one for long units, where half the bytes in flight still fill the
+// memory system and queue half as long).  After computing block k of unit U
+// it refills that buffer with stream position k + NB: U's own block, or one
+// of the first NB blocks of the next unit N, whose page ids (and, for one
+// query tile, query operand) are loaded a few blocks before U ends.  The
+// stream never drains between units; block k of a unit sits in buffer
+// (k + par) % NB, par carried over from unit to unit.
 //
 // An item of a single-split sequence writes the final output and LSE (and
 // marks split slot 0 with +inf for the merge); any other item writes its
 // fp32 partial (o / l, m, l) at its split slot.
-template <typename QT, int KT, int D, int NQT, bool TREE>
+template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
   typedef typename KvBlock<KT, D>::type Block;
@@ -309,6 +314,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // register set.  Two tiles: it is loaded once the current unit's last block
   // has been computed.
   constexpr bool kQPrefetch = NQT == 1;
+  static_assert(NB == 1 || NB == 2, "one or two blocks in flight per wave");
+  constexpr int kNeedLead = need_lead(NB);
+  constexpr int kPublishLead = publish_lead(NB);
+  constexpr int kClaimLead = claim_lead(NB);
 
   extern __shared__ int s_dyn[];  // compact mode: s_prefix[B + 1], s_len[B]
   __shared__ int s_pub[2][3];  // published item (b, s, L); b = -1: none
@@ -449,7 +458,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   };
 
   // ---- stream state (wave-uniform except the VGPR operands) ----
-  Block buf[2];
+  Block buf[NB];
   qvec8 qop[NQT][NS];
   qvec8 qopN[kQPrefetch ? NQT : 1][NS];
   int pidU = -1;
@@ -476,8 +485,9 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       pidU = (lane < tiles && lane < spec && v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
       const int nU = KT == 0 ? (tiles + 1) >> 1 : tiles;
       if (nU > 0) load_block(buf[0], pidU, wave, 0);
-      if (nU > 1) load_block(buf[1], pidU, wave, 1);
-      issuedU = min(nU, 2);
+      if constexpr (NB > 1)
+        if (nU > 1) load_block(buf[NB - 1], pidU, wave, 1);
+      issuedU = min(nU, NB);
       load_q(cb, wave, qop);
       load_tree(cb, treeU);
       u_loaded = true;
@@ -670,13 +680,17 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         issuedU = 0;
       }
       // top up the unit's first two blocks
-      if (issuedU < 1 && nU > 0) {
-        if (par) load_block(buf[1], pidU, kvh, 0);
-        else load_block(buf[0], pidU, kvh, 0);
-      }
-      if (issuedU < 2 && nU > 1) {
-        if (par) load_block(buf[0], pidU, kvh, 1);
-        else load_block(buf[1], pidU, kvh, 1);
+      if constexpr (NB == 1) {
+        if (issuedU < 1 && nU > 0) load_block(buf[0], pidU, kvh, 0);
+      } else {
+        if (issuedU < 1 && nU > 0) {
+          if (par) load_block(buf[NB - 1], pidU, kvh, 0);
+          else load_block(buf[0], pidU, kvh, 0);
+        }
+        if (issuedU < 2 && nU > 1) {
+          if (par) load_block(buf[0], pidU, kvh, 1);
+          else load_block(buf[NB - 1], pidU, kvh, 1);
+        }
       }
 
       // ---- the next unit of this wave ----
@@ -916,7 +930,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // the unit's own block or, in order, the next unit's first two blocks.
       auto step = [&](Block &r, int k) {
         compute_block(r, k);
-        const int pos = k + 2;
+        const int pos = k + NB;
         if (pos < nU) {
           load_block(r, pidU, kvh, pos);
         } else if (pos - nU == issuedN && issuedN < nN) {
@@ -932,15 +946,17 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           if (n_ready) set_next();
         }
       };
-      {
+      if constexpr (NB == 1) {
+        for (int k = 0; k < nU; ++k) step(buf[0], k);
+      } else {
         int k = 0;
         if (par && nU > 0) {
-          step(buf[1], 0);
+          step(buf[NB - 1], 0);
           k = 1;
         }
         for (; k + 1 < nU; k += 2) {
           step(buf[0], k);
-          step(buf[1], k + 1);
+          step(buf[NB - 1], k + 1);
         }
         if (k < nU) step(buf[0], k);
       }
@@ -1020,7 +1036,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       }
 
       // ---- the next unit inherits the stream ----
-      par = (par + nU) & 1;
+      par = (par + nU) % NB;
       pidU = pidN;
       if constexpr (TREE && kQPrefetch) treeU[0] = treeN[0];
       issuedU = issuedN;
@@ -1372,7 +1388,7 @@ bool partial_compact(int batch) { return batch <= l20pd::kMaxCompactBatch; }
 // at the kernel's occupancy, never more than there are split-major slots.
 // L20_PD_MAX_WORKGROUPS (a positive integer) caps the count, which lets tests
 // drive many items through each workgroup.
-template <typename QT, int KT, int D, int NQT, bool TREE>
+template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 int partial_grid(int threads, size_t lds, int64_t max_items) {
   static thread_local int cached_dev = -1, cached_threads = -1, cached_blocks = 0;  // per instantiation
   static thread_local size_t cached_lds = 0;
@@ -1381,7 +1397,7 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
   if (dev != cached_dev || threads != cached_threads || lds != cached_lds) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE>, threads,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE, NB>, threads,
                                                      lds) !=
             hipSuccess ||
         per_cu <= 0)
@@ -1399,26 +1415,35 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, max_items));
 }
 
-template <typename QT, int KT, int D, int NQT, bool TREE>
+template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 hipError_t launch_partial(l20pd::PartialParams pp, int batch, int num_kv_heads, hipStream_t stream) {
   const int nwaves = partial_waves(num_kv_heads);
   const int threads = 64 * nwaves;
   pp.compact = partial_compact(batch) ? 1 : 0;
   const size_t lds = pp.compact ? (size_t)(2 * batch + 1) * sizeof(int) : 0;
   const int64_t max_items = (int64_t)batch * pp.num_splits;
-  const int grid = partial_grid<QT, KT, D, NQT, TREE>(threads, lds, max_items);
-  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE>), dim3(grid), dim3(threads), lds, stream, pp);
+  const int grid = partial_grid<QT, KT, D, NQT, TREE, NB>(threads, lds, max_items);
+  hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE, NB>), dim3(grid), dim3(threads), lds, stream, pp);
   return hipGetLastError();
 }
 
 template <typename QT, int KT, bool TREE>
 hipError_t launch_partial_mask(const l20pd::PartialParams &pp, int head_dim, int nqt, int batch, int num_kv_heads,
                                hipStream_t stream) {
-  if (head_dim == 128)
-    return nqt == 1 ? launch_partial<QT, KT, 128, 1, TREE>(pp, batch, num_kv_heads, stream)
-                    : launch_partial<QT, KT, 128, 2, TREE>(pp, batch, num_kv_heads, stream);
-  return nqt == 1 ? launch_partial<QT, KT, 64, 1, TREE>(pp, batch, num_kv_heads, stream)
-                  : launch_partial<QT, KT, 64, 2, TREE>(pp, batch, num_kv_heads, stream);
+  if (head_dim == 128) {
+    // Units of up to 32 fp8 blocks (splits >= 1024): one block in flight per
+    // wave halves the bytes queued in the memory system at full bandwidth
+    // (verify shape 130.7 -> 126.4 us per call, long context 106.1 -> 104.5);
+    // shorter units keep two for the latency-bound end of the launch.
+    if constexpr (KT == 0)
+      if (pp.split_size >= 1024)
+        return nqt == 1 ? launch_partial<QT, KT, 128, 1, TREE, 1>(pp, batch, num_kv_heads, stream)
+                        : launch_partial<QT, KT, 128, 2, TREE, 1>(pp, batch, num_kv_heads, stream);
+    return nqt == 1 ? launch_partial<QT, KT, 128, 1, TREE, 2>(pp, batch, num_kv_heads, stream)
+                    : launch_partial<QT, KT, 128, 2, TREE, 2>(pp, batch, num_kv_heads, stream);
+  }
+  return nqt == 1 ? launch_partial<QT, KT, 64, 1, TREE, 2>(pp, batch, num_kv_heads, stream)
+                  : launch_partial<QT, KT, 64, 2, TREE, 2>(pp, batch, num_kv_heads, stream);
 }
 
 template <typename QT, int KT>

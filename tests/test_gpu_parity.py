@@ -231,6 +231,9 @@ QUEUE = [
     ("two_heads_per_wave", 3, 24, 12, 128, [900, 31, 400], 1, 128),
     ("three_heads_per_wave_d64", 2, 18, 9, 64, [500, 77], 1, 64),
     ("verify_q4", 4, 16, 2, 128, [700, 4, 130, 1500], 4, 96),
+    # splits of 1024 tokens: the one-block-in-flight stream (fp8, head_dim 128)
+    ("long_units_one_block", 4, 16, 2, 128, [5000, 33, 2048, 1100], 1, 1024),
+    ("long_units_verify_q4", 3, 32, 4, 128, [3000, 1030, 5], 4, 1024),
     # more sequences than the LDS prefix holds: split-major numbering with holes
     ("split_major_fallback", 600, 4, 1, 64, None, 1, 64),
 ]

@@ -47,6 +47,7 @@ TREE_SHAPES = [
     (2, 32, 32, 64, [530, 64], 8, 128),          # MHA, d=64
     (2, 4, 4, 128, [900, 32], 32, 256),          # 32 drafts, group 1, one sequence all drafts
     (4, 28, 4, 128, [2048, 17, 300, 4], 4, 512),  # Qwen-7B heads; one sequence holds only its drafts
+    (3, 64, 8, 128, [4096, 1500, 9], 4, 1024),   # verify heads, 1024-token splits (one block in flight)
 ]
 
 
