@@ -1210,6 +1210,74 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   }
 }
 
+// Narrow merge for at most kNarrowSlots split slots: lane l owns dims
+// [8c, 8c + 8) of one (query row, q head) pair (c = l % (D/8); 64 / (D/8)
+// pairs per wave) across every slot of it, so the fold needs no shuffles.
+// All slots below num_splits are read in the round trip that fetches the
+// sequence length (slots at or past the row's split count hold whatever an
+// earlier call left and are not folded).
+constexpr int kNarrowSlots = 8;
+template <typename QT, int D>
+__global__ __launch_bounds__(256) void pd_merge_narrow(MergeParams p) {
+  constexpr int CH = D / 8;     // 8-dim chunks per row
+  constexpr int PPW = 64 / CH;  // pairs per wave
+  const int lane = threadIdx.x & 63;
+  const int c = lane % CH;
+  const int64_t pair = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * PPW + lane / CH;
+  if (pair >= (int64_t)p.rows * p.num_q_heads) return;
+  const int row = (int)(pair / p.num_q_heads);
+  const int h = (int)(pair - (int64_t)row * p.num_q_heads);
+  const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
+  const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
+  const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
+  float ms[kNarrowSlots], ls[kNarrowSlots];
+  f32x4 o0[kNarrowSlots], o1[kNarrowSlots];
+#pragma unroll
+  for (int s = 0; s < kNarrowSlots; ++s) {
+    if (s < p.num_splits) {
+      ms[s] = pm[(int64_t)s * p.pm_ssplit];
+      ls[s] = pl[(int64_t)s * p.pl_ssplit];
+      const int64_t off = base + (int64_t)s * p.po_ssplit;
+      if (p.po_f32) {
+        const float *src = reinterpret_cast<const float *>(p.po) + off;
+        o0[s] = *reinterpret_cast<const f32x4 *>(src);
+        o1[s] = *reinterpret_cast<const f32x4 *>(src + 4);
+      } else {
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(p.po) + off);
+        o0[s] = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+        o1[s] = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+      }
+    }
+  }
+  const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
+  const int n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
+  if (n <= 1) return;                // the partial kernel wrote this row (or the empty row) directly
+  if (ms[0] == INFINITY) return;     // ... or marked it final
+  float mx = -INFINITY, wsum = 0.0f;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kNarrowSlots; ++s) {
+    if (s < n && ms[s] == ms[s] && ms[s] != -INFINITY) {
+      const float m_new = fmaxf(mx, ms[s]);
+      const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
+      const float w = __builtin_amdgcn_exp2f(ms[s] - m_new) * ls[s];
+      acc0 = acc0 * a_old + w * o0[s];
+      acc1 = acc1 * a_old + w * o1[s];
+      wsum = wsum * a_old + w;
+      mx = m_new;
+    }
+  }
+  const float inv = (wsum > 0.0f) ? 1.0f / wsum : 0.0f;
+  QT *dst = reinterpret_cast<QT *>(p.out) + (int64_t)row * p.o_srow + (int64_t)h * p.o_shead + 8 * c;
+  *reinterpret_cast<i32x4 *>(dst) = i32x4{pack2<QT>(acc0[0] * inv, acc0[1] * inv), pack2<QT>(acc0[2] * inv, acc0[3] * inv),
+                                          pack2<QT>(acc1[0] * inv, acc1[1] * inv), pack2<QT>(acc1[2] * inv, acc1[3] * inv)};
+  if (c == 0 && p.lse) {
+    const float msafe = (mx == -INFINITY) ? 0.0f : mx;
+    p.lse[(int64_t)row * p.lse_srow + (int64_t)h * p.lse_shead] =
+        (wsum > 0.0f) ? kLn2 * (msafe + __builtin_amdgcn_logf(wsum)) : -INFINITY;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Bulk dequantisers (same conversions as the attention kernel)
 // ---------------------------------------------------------------------------
@@ -1475,6 +1543,16 @@ int merge_waves_per_pair(int num_splits, int head_dim) {
 template <typename QT, int D>
 hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipStream_t stream) {
   const int64_t pairs = (int64_t)rows * heads;
+  if (mp.num_splits <= l20pd::kNarrowSlots && pairs >= 4096) {
+    // a few slots and many pairs (a bandwidth-heavy merge: verify shape 10.0 ->
+    // 7.4 us between the partial kernel and the end of the call): 64 / (D/8)
+    // pairs per wave, 4 waves per workgroup, one round trip.  Few pairs keep one
+    // wave per pair, which spreads a small merge over more waves.
+    const int64_t per_block = 4 * (64 / (D / 8));
+    hipLaunchKernelGGL((l20pd::pd_merge_narrow<QT, D>), dim3((unsigned)((pairs + per_block - 1) / per_block)), dim3(256),
+                       0, stream, mp);
+    return hipGetLastError();
+  }
   switch (merge_waves_per_pair(mp.num_splits, D)) {
     case 1: return launch_merge_wpp<QT, D, 1>(mp, pairs, stream);
     case 2: return launch_merge_wpp<QT, D, 2>(mp, pairs, stream);

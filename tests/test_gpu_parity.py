@@ -144,6 +144,37 @@ def test_merge_waves_per_pair(d, lens, split, pdt):
     H.compare(*H.run_op(inp, split, partial_dtype=pdt), *H.run_oracle(inp))
 
 
+@pytest.mark.parametrize("d,lens,split,pdt", [
+    (128, [4096, 4000, 1030, 5, 0], 1024, torch.float32),   # 4 slots, ragged rows
+    (64, [511, 300, 64, 1], 64, torch.float16),              # 8 slots (the narrow limit), fp16 partials
+    (128, [900, 2000], 256, torch.float32),                  # 8 slots, q_len 4 below
+])
+@pytest.mark.parametrize("q_len", [1, 4])
+def test_narrow_merge_ignores_stale_slots(d, lens, split, pdt, q_len):
+    """With at most 8 split slots and at least 4096 (row, head) pairs the merge
+    reads every slot with the length; slots past a row's split count hold
+    NaN / inf from an earlier call and must not count."""
+    import l20_pd_cabi as cabi
+
+    # 64 query heads: batch x q_len x 64 >= 4096 pairs for the narrow merge once
+    # the batch is filled up with short sequences (cheap for the oracle)
+    batch = 4096 // (64 * q_len)
+    lens = lens + [(37 * i) % 200 + q_len for i in range(batch - len(lens))]
+    inp = H.make_synthetic(batch, 64, 8, d, lens, q_len=q_len, seed=split + d + q_len)
+    po, pm, ps = H.workspace(inp, split, pdt)
+    for t, v in ((po, float("nan")), (pm, float("inf")), (ps, float("nan"))):
+        t.fill_(v)
+    q = inp["query"]
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device)
+    args = cabi.args_from_tensors(q, inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
+                                  po, pm, ps, out, inp["k_scale"], inp["v_scale"], inp["max_seq_len"], split,
+                                  softmax_scale=inp["softmax_scale"], q_len=q_len, lse=lse)
+    cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    H.compare(out, lse, *H.run_oracle(inp))
+
+
 def test_strided_kv_views_like_vllm_unbind():
     """vLLM's cache is [num_blocks, 2, 16, Hkv, D]; unbind(1) gives strided K/V views."""
     inp = H.make_synthetic(3, 16, 8, 128, [100, 1000, 37], seed=7)
