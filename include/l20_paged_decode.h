@@ -152,7 +152,9 @@ int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args);
 
 /* Enqueue the split-KV partial kernel and the LSE merge kernel on `stream`
  * (hipStream_t, NULL = default stream).  Asynchronous; allocates nothing.
- * Requires kv_dtype == L20_PD_KV_FP8_E4M3. */
+ * Requires kv_dtype == L20_PD_KV_FP8_E4M3.  Calls on different streams of one
+ * device may overlap (each with its own workspace and output): consecutive
+ * calls use different work-queue counters, 64 of them per device. */
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
 
 /* The fp16/bf16-KV sibling: the same two kernels over 16-bit caches

@@ -41,6 +41,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "l20_paged_decode.h"
@@ -107,6 +108,7 @@ struct PartialParams {
   const int32_t *indptr;  // CSR page list: sequence b's pages are bt[indptr[b] .. indptr[b + 1])
   const int32_t *tree;    // ancestor words [b * tree_sb + i] (bit j: row i sees draft key j), or NULL
   int64_t tree_sb;
+  int queue_slot;  // the launch's work-queue counters (g_pd_queue row)
 };
 
 // ---------------------------------------------------------------------------
@@ -248,12 +250,14 @@ __device__ __forceinline__ void lds_put(int *a, int v) {
 }
 
 __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
-// Work queue of the persistent partial kernel: [0] next queue item, [1]
-// workgroups finished.  Zero at load; the last workgroup to finish a launch
-// resets both, so every launch starts from zero without a memset (and a
-// captured graph replays correctly).  Launches on one device must therefore
-// not overlap.
-__device__ unsigned int g_pd_queue[2];
+// Work queues of the persistent partial kernel, one per launch slot (one
+// 64-byte line each): [0] next queue item, [1] workgroups finished.  Zero at
+// load; the last workgroup to finish a launch resets both, so every launch
+// starts from zero without a memset (and a captured graph replays
+// correctly).  The host gives consecutive launches consecutive slots, so up
+// to kQueueSlots launches may overlap on one device (different streams).
+constexpr int kQueueSlots = 64;
+__device__ __align__(64) unsigned int g_pd_queue[kQueueSlots][16];
 
 // Splits of sequence b taken by the static first round: workgroup w starts
 // on slot w of the split-major numbering (sequence w % B, split w / B).
@@ -593,7 +597,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   int t_item = 0;
   int nb = -1, ns = 0, nL = 0;
   auto issue_claim = [&]() {
-    if (lane == 0) claim = atomicAdd(&g_pd_queue[0], 1u);
+    if (lane == 0) claim = atomicAdd(&g_pd_queue[p.queue_slot][0], 1u);
     claimed = true;
   };
   auto claim_point = [&]() {
@@ -1064,10 +1068,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // counters order nothing else, and the kernel boundary publishes the reset
   // (a fence here would write back the XCD's L2).
   if (threadIdx.x == 0) {
-    const unsigned int done = atomicAdd(&g_pd_queue[1], 1u);
+    const unsigned int done = atomicAdd(&g_pd_queue[p.queue_slot][1], 1u);
     if (done == gridDim.x - 1) {
-      g_pd_queue[0] = 0u;
-      g_pd_queue[1] = 0u;
+      g_pd_queue[p.queue_slot][0] = 0u;
+      g_pd_queue[p.queue_slot][1] = 0u;
     }
   }
 }
@@ -1631,6 +1635,10 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.indptr = a.page_indptr;
   pp.tree = a.tree_mask;
   pp.tree_sb = a.tree_mask_stride_batch;
+  // consecutive launches take consecutive queue slots (launches that overlap
+  // on one device, from different streams, never share counters)
+  static std::atomic<unsigned int> launch_seq{0};
+  pp.queue_slot = (int)(launch_seq.fetch_add(1u, std::memory_order_relaxed) % l20pd::kQueueSlots);
   return pp;
 }
 

@@ -158,8 +158,15 @@ def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, part
     """Fill ``l20_pd_fp8_args`` from tensors (same argument order as the fp8 op).
 
     The cache dtype picks ``kv_dtype`` (fp8 e4m3fn, fp16 or bf16).  With
-    ``page_indptr`` [B+1], ``block_table`` is the flat CSR page list."""
+    ``page_indptr`` [B+1], ``block_table`` is the flat CSR page list.
+
+    The struct holds raw device pointers; it also keeps a reference to every
+    tensor it points into, so none of them is freed (and its memory handed to
+    another tensor by the caching allocator) while the struct is alive."""
     a = L20PdFp8Args()
+    a._tensors = tuple(t for t in (query, key_cache, value_cache, block_table, seq_lens, partial_output,
+                                   partial_max, partial_sum, output, k_scale_per_head, v_scale_per_head, lse,
+                                   page_indptr, tree_mask) if t is not None)
     a.kv_dtype = _kv_code(key_cache)
     a.query = query.data_ptr()
     a.query_dtype = _dtype_code(query)

@@ -89,6 +89,37 @@ def test_check_accepts_valid_arguments():
     cabi.check(valid_args())
 
 
+def test_args_from_tensors_keeps_its_tensors_alive():
+    """The struct holds raw pointers: the tensors behind them must outlive any
+    temporaries of the caller (a freed workspace would be handed to the next
+    allocation while the struct still points into it)."""
+    import gc
+    import weakref
+
+    import torch
+
+    q = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(10, 16, 2, 128, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    bt = torch.zeros(4, 4, dtype=torch.int32)
+    lens = torch.full((4,), 40, dtype=torch.int32)
+
+    def build():
+        po = torch.empty(4, 8, 2, 128)
+        pm, ps, out = torch.empty(4, 8, 2), torch.empty(4, 8, 2), torch.empty_like(q)
+        lse = torch.empty(4, 8)
+        refs = [weakref.ref(t) for t in (po, pm, ps, out, lse)]
+        return cabi.args_from_tensors(q, kc, kc, bt, lens, po, pm, ps, out, 1.0, 1.0, 64, 64, lse=lse), refs
+
+    a, refs = build()
+    gc.collect()
+    assert all(r() is not None for r in refs)
+    assert a.partial_output == refs[0]().data_ptr() and a.lse == refs[4]().data_ptr()
+    cabi.check(a)
+    del a
+    gc.collect()
+    assert all(r() is None for r in refs)
+
+
 BAD = [
     ("split_size", 48, "split_size must be a multiple of 16 from 64 through 1024"),
     ("split_size", 1040, "split_size must be a multiple of 16 from 64 through 1024"),

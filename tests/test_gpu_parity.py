@@ -175,6 +175,81 @@ def test_narrow_merge_ignores_stale_slots(d, lens, split, pdt, q_len):
     H.compare(out, lse, *H.run_oracle(inp))
 
 
+def test_launches_on_two_streams_overlap_safely():
+    """Two calls in flight on one device (two streams, each with its own
+    workspace) use different work-queue counters: results are bitwise those
+    of the calls run one at a time.  (The argument structs keep their
+    workspaces alive: the loop below rebinds the names.)"""
+    import l20_pd_cabi as cabi
+
+    cases = [H.make_synthetic(16, 16, 2, 128, [3000 - 97 * i for i in range(16)], seed=71),
+             H.make_synthetic(24, 28, 4, 128, [1500 + 61 * i for i in range(24)], seed=72)]
+    calls = []
+    for inp in cases:
+        po, pm, ps = H.workspace(inp, 256)
+        out = torch.empty_like(inp["query"])
+        lse = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+        args = cabi.args_from_tensors(inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                      inp["seq_lens"], po, pm, ps, out, inp["k_scale"], inp["v_scale"],
+                                      inp["max_seq_len"], 256, softmax_scale=inp["softmax_scale"], lse=lse)
+        calls.append((args, out, lse))
+    serial = []
+    for args, out, lse in calls:
+        cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        serial.append((out.clone(), lse.clone()))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for _ in range(20):
+        for (args, _, _), s in zip(calls, streams):
+            cabi.split_out(args, s.cuda_stream)
+    torch.cuda.synchronize()
+    for (_, out, lse), (s_out, s_lse) in zip(calls, serial):
+        assert torch.equal(out, s_out) and torch.equal(lse, s_lse)
+    for inp, (out, lse) in zip(cases, serial):
+        H.compare(out, lse, *H.run_oracle(inp))
+
+
+HOSTILE = [
+    # name, batch, hq, hkv, d, lens, max_wg (0: the full persistent grid)
+    ("all_static_items", 16, 16, 2, 128, [3000 - 97 * i for i in range(16)], 0),
+    ("queue_items", 24, 28, 4, 128, [1500 + 61 * i for i in range(24)], 5),
+    ("one_split_rows", 6, 16, 2, 128, [3000, 1, 256, 0, 257, 40], 0),
+]
+
+
+@pytest.mark.parametrize("case", HOSTILE, ids=[c[0] for c in HOSTILE])
+def test_results_do_not_depend_on_prior_buffer_contents(case, monkeypatch):
+    """Workspace, output and LSE buffers come from ``torch.empty``: whatever a
+    call reads it has written itself, so NaN, infinite or huge prior contents
+    (including +inf in slot 0, the merge's "already final" marker) change
+    nothing, bitwise."""
+    import l20_pd_cabi as cabi
+
+    name, batch, hq, hkv, d, lens, max_wg = case
+    if max_wg:
+        monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", str(max_wg))
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, seed=zlib.crc32(name.encode()) % 1000)
+    exp = H.run_oracle(inp)
+    po, pm, ps = H.workspace(inp, 256, extra_splits=2)
+    out = torch.empty_like(inp["query"])
+    lse = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+    args = cabi.args_from_tensors(inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                  inp["seq_lens"], po, pm, ps, out, inp["k_scale"], inp["v_scale"],
+                                  inp["max_seq_len"], 256, softmax_scale=inp["softmax_scale"], lse=lse)
+    first = None
+    for fill in (float("nan"), float("inf"), float("-inf"), 3e38, -3e38, 0.0):
+        for t in (po, pm, ps, lse):
+            t.fill_(fill)
+        out.fill_(fill if fill == fill and abs(fill) < 1e38 else 0.0)
+        cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        H.compare(out, lse, *exp)
+        if first is None:
+            first = (out.clone(), lse.clone())
+        else:
+            assert torch.equal(out, first[0]) and torch.equal(lse, first[1]), f"prior contents {fill} changed the result"
+
+
 def test_strided_kv_views_like_vllm_unbind():
     """vLLM's cache is [num_blocks, 2, 16, Hkv, D]; unbind(1) gives strided K/V views."""
     inp = H.make_synthetic(3, 16, 8, 128, [100, 1000, 37], seed=7)
