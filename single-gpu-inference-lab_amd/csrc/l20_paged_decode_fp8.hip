@@ -251,11 +251,17 @@ __device__ __forceinline__ void lds_put(int *a, int v) {
 
 __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
 // Work queues of the persistent partial kernel, one per launch slot (one
-// 64-byte line each): [0] next queue item, [1] workgroups finished.  Zero at
-// load; the last workgroup to finish a launch resets both, so every launch
-// starts from zero without a memset (and a captured graph replays
-// correctly).  The host gives consecutive launches consecutive slots, so up
-// to kQueueSlots launches may overlap on one device (different streams).
+// 64-byte line each; word 0 is the next queue item).  Zero at load.  A launch
+// whose grid covers every split-major slot claims nothing.  Otherwise every
+// workgroup claims until a claim fails (returns >= Q, the queue length), so
+// exactly gridDim.x claims fail and the one that returns Q + gridDim.x - 1 is
+// the last atomic on the counter in this launch: its workgroup resets the
+// counter, and every launch starts from zero without a memset (a captured
+// graph replays correctly).  Claims on one line are served one at a time
+// (~11 ns each on MI355X), which is why nothing else (such as a count of
+// finished workgroups) shares it.  The host gives consecutive launches
+// consecutive slots, so up to kQueueSlots launches may overlap on one device
+// (different streams).
 constexpr int kQueueSlots = 64;
 __device__ __align__(64) unsigned int g_pd_queue[kQueueSlots][16];
 
@@ -593,7 +599,9 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // rewrites a slot only after every other wave has acknowledged it.
   unsigned int claim = 0;
   bool claimed = false;  // wave 0: a claim is in flight
-  bool more = true;      // wave 0: the queue may still hold items
+  // wave 0: the queue may still hold items (never, when the static round
+  // covers every slot: then no workgroup claims)
+  bool more = (int64_t)G < (int64_t)B * p.num_splits;
   int t_item = 0;
   int nb = -1, ns = 0, nL = 0;
   auto issue_claim = [&]() {
@@ -616,6 +624,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       claimed = false;
       if (c >= Q) {
         more = false;
+        // the launch's last claim: no other atomic on the counter follows
+        if (lane == 0 && c == Q + G - 1) g_pd_queue[p.queue_slot][0] = 0u;
         return;
       }
       if (decode(c)) return;
@@ -656,7 +666,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     return true;
   };
 
-  if (compact && wave == nwaves - 1) {
+  if (compact && more && wave == nwaves - 1) {
     build_prefix();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the flag follows the table (LDS operations of a wave execute in order)
     if (lane == 0) lds_put(&s_prefix_ready, 1);
@@ -1063,17 +1073,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     cL = nL;
     ++t_item;
   }
-  // ---- end of the launch: the last workgroup out resets the queue ----
-  // Every claim of this workgroup has been resolved by now.  No fence: the
-  // counters order nothing else, and the kernel boundary publishes the reset
-  // (a fence here would write back the XCD's L2).
-  if (threadIdx.x == 0) {
-    const unsigned int done = atomicAdd(&g_pd_queue[p.queue_slot][1], 1u);
-    if (done == gridDim.x - 1) {
-      g_pd_queue[p.queue_slot][0] = 0u;
-      g_pd_queue[p.queue_slot][1] = 0u;
-    }
-  }
+  // Every claim of this workgroup has been resolved by now; the counter was
+  // reset by the launch's last claim.  No fence: the counter orders nothing
+  // else, and the kernel boundary publishes the reset (a fence would write
+  // back the XCD's L2).
 }
 
 // ---------------------------------------------------------------------------

@@ -293,9 +293,15 @@ def test_hook_api_with_auto_split_and_reused_workspace():
     H.compare(out, None, exp[0], None, check_lse=False)
 
 
-def test_hip_graph_capture_replays_match_eager():
+@pytest.mark.parametrize("max_wg", [0, 5], ids=["static_grid", "queue"])
+def test_hip_graph_capture_replays_match_eager(max_wg, monkeypatch):
+    """Replays reuse the captured launch's work-queue slot: with a 5-workgroup
+    grid every replay drains a queue and must find its counter reset by the
+    previous replay's last claim."""
     import l20_paged_decode  # noqa: F401
 
+    if max_wg:
+        monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", str(max_wg))
     inp = H.make_synthetic(4, 28, 4, 128, [3000, 700, 64, 1500], seed=10)
     po, pm, ps = H.workspace(inp, 256)
     out = torch.empty_like(inp["query"])
@@ -319,13 +325,45 @@ def test_hip_graph_capture_replays_match_eager():
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         call()
-    for _ in range(3):
+    for _ in range(4):
         out.zero_()
         lse.zero_()
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager_out) and torch.equal(lse, eager_lse)
+    H.compare(eager_out, eager_lse, *H.run_oracle(inp))
+
+
+def test_queue_counters_reset_across_slot_reuse(monkeypatch):
+    """150 back-to-back queue-driven launches wrap the 64 work-queue slots
+    twice; each launch must start on a counter its slot's previous launch
+    reset (a stale counter would skip items and change the result)."""
+    import l20_pd_cabi as cabi
+
+    monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", "7")
+    inp = H.make_synthetic(6, 16, 2, 128, [2100, 17, 900, 0, 1300, 64], seed=12)
+    exp = H.run_oracle(inp)
+    po, pm, ps = H.workspace(inp, 64)
+    out = torch.empty_like(inp["query"])
+    lse = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+    args = cabi.args_from_tensors(inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                  inp["seq_lens"], po, pm, ps, out, inp["k_scale"], inp["v_scale"],
+                                  inp["max_seq_len"], 64, softmax_scale=inp["softmax_scale"], lse=lse)
+    stream = torch.cuda.current_stream().cuda_stream
+    cabi.split_out(args, stream)
+    torch.cuda.synchronize()
+    H.compare(out, lse, *exp)
+    first = (out.clone(), lse.clone())
+    outs = torch.empty((150,) + tuple(out.shape), dtype=out.dtype, device="cuda")
+    lses = torch.empty((150,) + tuple(lse.shape), dtype=lse.dtype, device="cuda")
+    for i in range(150):
+        cabi.split_out(args, stream)
+        outs[i].copy_(out)
+        lses[i].copy_(lse)
+    torch.cuda.synchronize()
+    bad = [i for i in range(150) if not (torch.equal(outs[i], first[0]) and torch.equal(lses[i], first[1]))]
+    assert not bad, f"launches {bad[:10]} differ from the first"
 
 
 # ------------------------------------------------------------ work queue
