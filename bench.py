@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--hot", action="store_true", help="reuse one input set (cache-warm, informational)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--partial-dtype", choices=["fp32", "fp16"], default="fp32",
+                    help="split-partial workspace dtype (the op accepts both; fp32 is the default)")
     ap.add_argument("--cpu-sample", type=int, default=0, help="sequences (tokens for kv_write) in the CPU sample")
     return ap.parse_args()
 
@@ -230,7 +232,8 @@ def run_decode(args, mode):
 
     calls = []
     for s in sets:
-        po = torch.empty(rows, cfg.num_q_heads, n_s, cfg.head_dim, dtype=torch.float32, device=dev)
+        po = torch.empty(rows, cfg.num_q_heads, n_s, cfg.head_dim,
+                         dtype=torch.float16 if args.partial_dtype == "fp16" else torch.float32, device=dev)
         pm = torch.empty(rows, cfg.num_q_heads, n_s, dtype=torch.float32, device=dev)
         ps = torch.empty_like(pm)
         out = torch.empty_like(s["query"])
@@ -330,6 +333,7 @@ def run_decode(args, mode):
             "mask": "tree (random ancestor words per sequence)" if mode == "tree" else (
                 "causal over the q_len new tokens" if cfg.q_len > 1 else "none"),
             "split_size": split,
+            "partial_dtype": args.partial_dtype,
             "kv_bytes_per_call": int(bytes_per_step),
             "input_sets": n_sets,
             "cache_state": "hot (one set)" if args.hot else (
