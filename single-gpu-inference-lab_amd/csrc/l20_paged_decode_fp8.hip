@@ -68,6 +68,10 @@ constexpr int need_lead(int nb) { return nb + 1; }
 constexpr int publish_lead(int nb) { return nb + 4; }
 constexpr int claim_lead(int nb) { return nb + 7; }
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: dword 3 (format bits)
+// Cache policy of the K/V stream loads: non-temporal (the CPol NT bit).  Every
+// K/V byte is read once per call; on MI355X a streaming read with NT reaches
+// ~7.1 TB/s against ~6.35 TB/s with the default policy.
+constexpr int kStreamPolicy = 2;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleLog2 = 8.0f;  // lazy online-softmax rescale threshold (log2 units)
@@ -430,15 +434,15 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        r.k[s] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), 0));
+        r.k[s] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), kStreamPolicy));
       const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if constexpr (D == 128)
-          r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, 0));
+          r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, kStreamPolicy));
         else
-          r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, 0));
+          r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
       }
       return;
     }
@@ -453,15 +457,15 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, 0));
+        r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, kStreamPolicy));
       const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if constexpr (D == 128)
-          r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, 0));
+          r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
         else
-          r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, 0);
+          r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, kStreamPolicy);
       }
     }
     }
@@ -1351,7 +1355,7 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t *src, in
     i32x4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      v[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + u * kStep, 0, 0));
+      v[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + u * kStep, 0, kStreamPolicy));
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
   }
