@@ -351,6 +351,15 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   const int G = gridDim.x;
   const int hpw = p.num_kv_heads / nwaves;  // units per item and wave
   const bool compact = p.compact != 0;
+  // Items beyond the split-major slots of the grid go through the queue.
+  // Then, in compact mode, only workgroups [0, G1) start on a split-major
+  // slot (one per CU: the first workgroup dispatched to each); workgroup
+  // w >= G1 starts on queue item w - G1 of the compact numbering without a
+  // claim.  Its page ids need the LDS prefix first, but as the second
+  // workgroup on its CU its first loads would queue behind the first one's
+  // K/V burst anyway, and no queue item waits for a claim in the first round.
+  const bool queued = (int64_t)G < (int64_t)B * p.num_splits;
+  const int G1 = (compact && queued) ? (G + 1) / 2 : G;
   int *s_prefix = s_dyn;      // s_prefix[b]: queue items of sequences < b
   int *s_len = s_dyn + B + 1;  // clamped length of sequence b
 
@@ -485,8 +494,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // ---- static first item: slot blockIdx.x of the split-major numbering ----
   int cb = (int)(blockIdx.x % (unsigned)B);
   int cs = (int)(blockIdx.x / (unsigned)B);
-  int cL;
-  {
+  int cL = 0;
+  if ((int)blockIdx.x >= G1) {
+    cb = -2;  // starts on queue item blockIdx.x - G1
+  } else {
     // Page ids and the length leave together; the ids are masked to the
     // split once the length is known.
     const int start = cs * S;
@@ -539,7 +550,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         if (e0 + e < per && idx < B) {
           const int L = max(0, min(lv[e], p.l_cap));
           s_len[idx] = L;
-          sum += max(0, splits_of_len(L, S) - static_splits(idx, G, B));
+          sum += max(0, splits_of_len(L, S) - static_splits(idx, G1, B));
         }
       }
     }
@@ -553,7 +564,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     for (int e = 0; e < per; ++e) {
       const int idx = lane * per + e;
       if (idx < B) {
-        run += max(0, splits_of_len(s_len[idx], S) - static_splits(idx, G, B));
+        run += max(0, splits_of_len(s_len[idx], S) - static_splits(idx, G1, B));
         s_prefix[idx + 1] = run;
       }
     }
@@ -578,7 +589,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       const uint64_t m2 = __ballot(lane < chunk && idx < B && s_prefix[idx] <= ci);
       const int b = base + __popcll(m2) - 1;
       db = b;
-      ds = static_splits(b, G, B) + (ci - lds_uniform(s_prefix, b));
+      ds = static_splits(b, G1, B) + (ci - lds_uniform(s_prefix, b));
       dL = lds_uniform(s_len, b);
       return true;
     }
@@ -601,15 +612,18 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // blocks before their unit ends); they then start prefetching it.  No
   // barrier separates items: each reader acknowledges the slot, and wave 0
   // rewrites a slot only after every other wave has acknowledged it.
-  unsigned int claim = 0;
-  bool claimed = false;  // wave 0: a claim is in flight
+  // wave 0: a claim is in flight (a workgroup past the split-major round
+  // holds queue item blockIdx.x - G1 as if claimed; atomic claims number
+  // the items after those)
+  unsigned int claim = (int)blockIdx.x >= G1 ? blockIdx.x - (unsigned)G1 : 0u;
+  bool claimed = (int)blockIdx.x >= G1;
   // wave 0: the queue may still hold items (never, when the static round
   // covers every slot: then no workgroup claims)
-  bool more = (int64_t)G < (int64_t)B * p.num_splits;
+  bool more = queued;
   int t_item = 0;
   int nb = -1, ns = 0, nL = 0;
   auto issue_claim = [&]() {
-    if (lane == 0) claim = atomicAdd(&g_pd_queue[p.queue_slot][0], 1u);
+    if (lane == 0) claim = atomicAdd(&g_pd_queue[p.queue_slot][0], 1u) + (unsigned)(G - G1);
     claimed = true;
   };
   auto claim_point = [&]() {
@@ -628,7 +642,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       claimed = false;
       if (c >= Q) {
         more = false;
-        // the launch's last claim: no other atomic on the counter follows
+        // The launch's last atomic claim: no other atomic on the counter
+        // follows.  Every workgroup stops at its first failure; those past
+        // the split-major round whose pre-assigned item fails make no atomic
+        // claim, and either way the last atomic returns Q + G - 1 (after the
+        // G - G1 offset; a pre-assigned failure is at most G - 1 - G1).
         if (lane == 0 && c == Q + G - 1) g_pd_queue[p.queue_slot][0] = 0u;
         return;
       }
