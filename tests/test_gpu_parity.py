@@ -369,6 +369,8 @@ def test_queue_counters_reset_across_slot_reuse(monkeypatch):
 # ------------------------------------------------------------ work queue
 # L20_PD_MAX_WORKGROUPS caps the persistent grid, so each workgroup streams
 # many items (and unit-to-unit prefetch crosses items of different sequences).
+# With items left over, workgroups [G/2, G) start on pre-assigned items of the
+# compact numbering: grids of 2, 3 and 5 put 1, 1 and 2 workgroups there.
 QUEUE = [
     # name, batch, hq, hkv, d, lens, q_len, split
     ("compact_ragged", 8, 16, 2, 128, [3000, 0, 17, 700, 64, 1, 2049, 333], 1, 64),
@@ -384,7 +386,7 @@ QUEUE = [
 
 
 @pytest.mark.parametrize("case", QUEUE, ids=[c[0] for c in QUEUE])
-@pytest.mark.parametrize("max_wg", [1, 3, 0])
+@pytest.mark.parametrize("max_wg", [1, 2, 3, 5, 0])
 def test_work_queue_small_grids(case, max_wg, monkeypatch):
     name, batch, hq, hkv, d, lens, q_len, split = case
     if lens is None:
