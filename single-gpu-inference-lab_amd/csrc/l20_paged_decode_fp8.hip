@@ -432,26 +432,31 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // and compute_block zeroes V of every token outside the split or on an
   // invalid page.  Lane offsets inside a page fit in 32 bits (checked on the
   // host).
-  auto load_block = [&](Block &r, int pid, int kvh, int blk) {
+  // parts: 1 = the K loads, 2 = the V loads, 3 = both (a constant at every call)
+  auto load_block = [&](Block &r, int pid, int kvh, int blk, int parts = 3) {
     if constexpr (KT == 1) {
       // 16-bit elements: one page per block; K slice s at byte 128*(s/2) + 16*(s%2)
       const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 32 * j);
       const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + 2 * (D / 16) * n16);
       const int raw_page = __builtin_amdgcn_readlane(pid, blk);
       const int page = raw_page >= 0 ? raw_page : 0;
-      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+      if (parts & 1) {
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        r.k[s] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), kStreamPolicy));
-      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+        for (int s = 0; s < NS; ++s)
+          r.k[s] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), kStreamPolicy));
+      }
+      if (parts & 2) {
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (D == 128)
-          r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, kStreamPolicy));
-        else
-          r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (D == 128)
+            r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, kStreamPolicy));
+          else
+            r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
+        }
       }
       return;
     }
@@ -462,19 +467,23 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     for (int T = 0; T < 2; ++T) {
       const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
       const int page = raw_page >= 0 ? raw_page : 0;
-      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+      if (parts & 1) {
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, kStreamPolicy));
-      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+        for (int c = 0; c < NCH; ++c)
+          r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, kStreamPolicy));
+      }
+      if (parts & 2) {
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (D == 128)
-          r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
-        else
-          r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, kStreamPolicy);
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (D == 128)
+            r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
+          else
+            r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, kStreamPolicy);
+        }
       }
     }
     }
@@ -791,7 +800,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 
-      auto compute_block = [&](Block &r, int blk) {
+      auto compute_block = [&](Block &r, int blk, auto &&after_scores) {
         const int tok0 = uStart + kTok * blk;
         // Tokens past the split (the tail of the sequence's last page, or a
         // tile beyond the split read from page 0) and tokens of an invalid
@@ -853,6 +862,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
             for (int qt = 0; qt < NQT; ++qt) sc[qt][0] = mfma16(kop, qop[qt][s], sc[qt][0]);
           }
         }
+        // r.k is consumed: the refill's K loads may overwrite it
+        after_scores();
         // ---- online softmax (log2 domain) ----
         const bool need_mask = (tok0 + kTok - 1 > min_lim) || bad0 || bad1;
         pvec8 pop[NQT];
@@ -965,12 +976,27 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // Compute block k, then refill its buffer with stream position k + 2:
       // the unit's own block or, in order, the next unit's first two blocks.
       auto step = [&](Block &r, int k) {
-        compute_block(r, k);
+        // The refill of r: block k + NB of this unit, or of the next.  With
+        // two blocks in flight it is issued in two parts, its K loads as soon
+        // as the scores of block k have consumed r.k and its V loads after
+        // the V^T.P^T product, so the softmax and PV of block k overlap the
+        // refill's K latency (config 3 49.6 -> 49.2 us, bf16 caches 89.1 ->
+        // 88.3).  With one block in flight the split cost 0.5-3.9 us (long
+        // context, verify, tree), so K and V leave together after the block.
         const int pos = k + NB;
-        if (pos < nU) {
-          load_block(r, pidU, kvh, pos);
-        } else if (pos - nU == issuedN && issuedN < nN) {
-          load_block(r, pidN, nKvh, issuedN);
+        const bool own = pos < nU;
+        const bool nxt = !own && pos - nU == issuedN && issuedN < nN;
+        compute_block(r, k, [&]() {
+          if constexpr (NB > 1) {
+            if (own) load_block(r, pidU, kvh, pos, 1);
+            else if (nxt) load_block(r, pidN, nKvh, issuedN, 1);
+          }
+        });
+        constexpr int kLate = NB > 1 ? 2 : 3;  // the parts left for after the block
+        if (own) {
+          load_block(r, pidU, kvh, pos, kLate);
+        } else if (nxt) {
+          load_block(r, pidN, nKvh, issuedN, kLate);
           ++issuedN;
         }
         if (k == k_claim) claim_point();
