@@ -1,0 +1,71 @@
+"""GPU parity over a seeded random sweep of shapes.
+
+Each case draws a batch, head layout, head_dim, q_len, cache dtype, scale
+kind, ragged lengths (empty sequences and page-boundary lengths included),
+split size and workspace dtype from a fixed seed, runs the op, and compares
+with the CPU oracle at the tolerances in ``pd_helpers``.  Sizes stay small so
+that the oracle finishes each case in well under a second.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import pd_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 120
+SPLITS = [64, 96, 128, 256, 512, 1024]
+HEADS = [(4, 4), (8, 2), (14, 2), (16, 8), (28, 4), (32, 4)]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X GPU")
+    import l20_paged_decode  # noqa: F401  (fails loudly if the extension is missing)
+
+
+def draw(case):
+    rng = np.random.default_rng(1000 + case)
+    hq, hkv = HEADS[rng.integers(len(HEADS))]
+    d = int(rng.choice([64, 128]))
+    q_len = int(rng.choice([1, 1, 2, 4]))
+    if (hq // hkv) * q_len > 32:
+        q_len = 1
+    batch = int(rng.integers(1, 9))
+    kind = rng.integers(4)
+    if kind == 0:  # short and ragged around page boundaries
+        lens = rng.choice([0, 1, 15, 16, 17, 31, 32, 33, 63, 64, 65], size=batch)
+    elif kind == 1:  # medium
+        lens = rng.integers(1, 1500, size=batch)
+    elif kind == 2:  # one long, the rest short
+        lens = rng.integers(0, 100, size=batch)
+        lens[rng.integers(batch)] = rng.integers(2000, 5000)
+    else:  # equal lengths
+        lens = np.full(batch, int(rng.integers(100, 3000)))
+    lens = [max(int(x), q_len if x > 0 else 0) for x in lens]
+    return dict(hq=hq, hkv=hkv, d=d, q_len=q_len, batch=batch, lens=lens,
+                cache=str(rng.choice(["fp8", "fp8", "fp16", "bf16"])),
+                per_head=bool(rng.integers(2)),
+                split=int(rng.choice(SPLITS)),
+                partial=str(rng.choice(["fp32", "fp32", "fp16"])),
+                seed=int(rng.integers(1 << 30)))
+
+
+@pytest.mark.parametrize("case", range(N_CASES))
+def test_random_shape(case):
+    c = draw(case)
+    pdt = torch.float16 if c["partial"] == "fp16" else torch.float32
+    print(case, c, flush=True)
+    if c["cache"] == "fp8":
+        inp = H.make_synthetic(c["batch"], c["hq"], c["hkv"], c["d"], c["lens"], q_len=c["q_len"],
+                               per_head=c["per_head"], seed=c["seed"], garbage_tail=True)
+        H.compare(*H.run_op(inp, c["split"], partial_dtype=pdt), *H.run_oracle(inp))
+    else:
+        dtype = torch.float16 if c["cache"] == "fp16" else torch.bfloat16
+        inp = H.make_synthetic16(c["batch"], c["hq"], c["hkv"], c["d"], c["lens"], dtype=dtype,
+                                 q_len=c["q_len"], seed=c["seed"], garbage_tail=True, csr_pad=1)
+        csr = bool(c["seed"] & 1)
+        H.compare(*H.run_op16(inp, c["split"], csr=csr, partial_dtype=pdt), *H.run_oracle16(inp, csr=csr))
