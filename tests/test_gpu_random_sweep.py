@@ -2,7 +2,8 @@
 
 Each case draws a batch, head layout, head_dim, q_len, cache dtype, scale
 kind, ragged lengths (empty sequences and page-boundary lengths included),
-split size and workspace dtype from a fixed seed, runs the op, and compares
+split size, workspace dtype and (fp8, q_len > 1) arbitrary tree-mask words
+from a fixed seed, runs the op, and compares
 with the CPU oracle at the tolerances in ``pd_helpers``.  Sizes stay small so
 that the oracle finishes each case in well under a second.
 """
@@ -51,7 +52,8 @@ def draw(case):
                 per_head=bool(rng.integers(2)),
                 split=int(rng.choice(SPLITS)),
                 partial=str(rng.choice(["fp32", "fp32", "fp16"])),
-                seed=int(rng.integers(1 << 30)))
+                seed=int(rng.integers(1 << 30)),
+                tree=bool(q_len > 1 and rng.integers(2)))
 
 
 @pytest.mark.parametrize("case", range(N_CASES))
@@ -62,6 +64,9 @@ def test_random_shape(case):
     if c["cache"] == "fp8":
         inp = H.make_synthetic(c["batch"], c["hq"], c["hkv"], c["d"], c["lens"], q_len=c["q_len"],
                                per_head=c["per_head"], seed=c["seed"], garbage_tail=True)
+        if c["tree"]:  # arbitrary ancestor words over the q_len drafts, one row per (sequence, draft)
+            w = np.random.default_rng(c["seed"]).integers(0, 2**32, size=(c["batch"], c["q_len"]), dtype=np.int64)
+            inp["tree_mask"] = torch.from_numpy(np.where(w >= 2**31, w - 2**32, w).astype(np.int32)).cuda()
         H.compare(*H.run_op(inp, c["split"], partial_dtype=pdt), *H.run_oracle(inp))
     else:
         dtype = torch.float16 if c["cache"] == "fp16" else torch.bfloat16
