@@ -126,12 +126,16 @@ def oracle_call(inp, rows):
     return res, int(sl.sum()), kc.shape, time.perf_counter() - t0
 
 
-def cpu_baseline_decode(inp, cfg, sample_seqs, elem_bytes):
-    """Time the CPU oracle over the first ``sample_seqs`` sequences of one input set."""
+def cpu_baseline_decode(inp, cfg, sample_seqs, elem_bytes, min_seconds=10.0):
+    """Time the CPU oracle over the first ``sample_seqs`` sequences of one input
+    set: at least three calls, repeated until ``min_seconds`` of CPU work (at
+    most 50 calls); the median call gives the rate."""
     import l20_pd_workloads as wl
 
     rows = list(range(sample_seqs))
-    times = [oracle_call(inp, rows)[3] for _ in range(3)]
+    times = []
+    while len(times) < 3 or (sum(times) < min_seconds and len(times) < 50):
+        times.append(oracle_call(inp, rows)[3])
     t = statistics.median(times)
     sl = inp["seq_lens"][:sample_seqs].cpu()
     kv = wl.kv_bytes(sl, cfg.num_kv_heads, cfg.head_dim, elem_bytes)
@@ -141,8 +145,8 @@ def cpu_baseline_decode(inp, cfg, sample_seqs, elem_bytes):
         "cores": int(threads_in_use()),
         "kind": "port",
         "sample": f"numpy oracle (oracle/paged_fp8_decode_ref.py) over sequences 0..{sample_seqs - 1} of the "
-                  f"workload ({int(sl.sum())} tokens, {kv / 1e6:.1f} MB KV), median of 3, "
-                  f"{t * 1e3:.1f} ms per sample call",
+                  f"workload ({int(sl.sum())} tokens, {kv / 1e6:.1f} MB KV), median of {len(times)} calls "
+                  f"({sum(times):.1f} s of CPU work), {t * 1e3:.1f} ms per sample call",
         "us_per_call_sample": round(t * 1e6, 1),
     }
 
@@ -312,7 +316,7 @@ def run_decode(args, mode):
 
     cpu = None
     if not args.no_cpu_baseline:
-        sample = args.cpu_sample or min(cfg.batch, 32 if mode == "decode" else 4)
+        sample = args.cpu_sample or (cfg.batch if mode == "decode" else min(cfg.batch, 4))
         cpu = cpu_baseline_decode(first, cfg, sample, elem)
 
     workload = cfg.name + {"decode": "", "decode16": "+bf16kv", "tree": "+tree"}[mode]
@@ -484,15 +488,17 @@ def run_kv_write(args):
 
     cpu = None
     if not args.no_cpu_baseline:
-        n = args.cpu_sample or 512
-        times = [oracle_sample(n)[1] for _ in range(3)]
+        n = args.cpu_sample or 4096
+        times = []  # at least three calls, up to ~10 s of CPU work (at most 50 calls)
+        while len(times) < 3 or (sum(times) < 10.0 and len(times) < 50):
+            times.append(oracle_sample(n)[1])
         t = statistics.median(times)
         sample_bytes = kv_write_bytes(dict(c, tokens=n))
         cpu = {"value": round(sample_bytes / t / 1e9, 4), "unit": "GB/s", "cores": int(threads_in_use()),
                "kind": "port",
                "sample": f"numpy oracle (oracle/kv_write_ref.py) over the first {n} tokens of the chunk "
-                         f"({sample_bytes / 1e6:.1f} MB of algorithmic traffic), median of 3, "
-                         f"{t * 1e3:.1f} ms per sample call"}
+                         f"({sample_bytes / 1e6:.1f} MB of algorithmic traffic), median of {len(times)} calls "
+                         f"({sum(times):.1f} s of CPU work), {t * 1e3:.1f} ms per sample call"}
 
     return {
         "metric": METRICS["kv_write"],
