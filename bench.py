@@ -164,7 +164,7 @@ def measured_traffic(workload: str, split: int, kernel: str = "pd_fp8_partial"):
             read = e["fetch_kib"] * 1024 * data["fetch_scale"]
             write = e["write_kib"] * 1024 * data["write_scale"]
             return {"bytes": int(read + write), "read_bytes": int(read), "write_bytes": int(write),
-                    "source": data["source"]}
+                    "source": e.get("source", data["source"])}
     return None
 
 
