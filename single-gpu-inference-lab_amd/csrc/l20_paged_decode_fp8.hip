@@ -1148,7 +1148,7 @@ struct MergeParams {
 };
 
 // WPP waves per (query row, q head) pair (WPP = 1, 2, 4, 8 or 16: enough
-// that each wave holds at most two steps of slots).  Lane l of a wave owns
+// that each wave holds at most four steps of slots).  Lane l of a wave owns
 // dims [8c, 8c + 8) of slot group g (c = l % (D/8), g = l / (D/8)); wave w of
 // a pair takes slots (w + WPP * step) * G + g, G = 512/D groups, so every load
 // of a wave is independent and issued together.  Each wave folds its groups
@@ -1185,29 +1185,41 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
   const int n_here = n > 1 ? n : 0;
-#pragma unroll 2
-  for (int s0 = wp * SG; s0 < n_here; s0 += WPP * SG) {
-    const int s = s0 + g;
-    if (s < n_here) {
-      const float ms = pm[(int64_t)s * p.pm_ssplit];
-      const float ls = pl[(int64_t)s * p.pl_ssplit];
-      const int64_t off = base + (int64_t)s * p.po_ssplit;
-      f32x4 o0, o1;
+  // Steps of a wave in groups of kSteps: every load of a group is issued
+  // before the group is folded (one round trip for up to kSteps steps); a
+  // slot past the row's count loads slot 0, which exists whenever n > 1, and
+  // is not folded.  (Against a loop unrolled by two with the loads under the
+  // slot test: call minus partial kernel 5.76 -> 5.57 us at config 3, 8.2 ->
+  // 7.65 us at config 4.)
+  constexpr int kSteps = 4;
+  for (int s0 = wp * SG; s0 < n_here; s0 += kSteps * WPP * SG) {
+    float ms[kSteps], ls[kSteps];
+    f32x4 o0[kSteps], o1[kSteps];
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      const int s = s0 + k * WPP * SG + g;
+      const int sl = s < n_here ? s : 0;
+      ms[k] = pm[(int64_t)sl * p.pm_ssplit];
+      ls[k] = pl[(int64_t)sl * p.pl_ssplit];
+      const int64_t off = base + (int64_t)sl * p.po_ssplit;
       if (p.po_f32) {
         const float *src = reinterpret_cast<const float *>(p.po) + off;
-        o0 = *reinterpret_cast<const f32x4 *>(src);
-        o1 = *reinterpret_cast<const f32x4 *>(src + 4);
+        o0[k] = *reinterpret_cast<const f32x4 *>(src);
+        o1[k] = *reinterpret_cast<const f32x4 *>(src + 4);
       } else {
         const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(p.po) + off);
-        o0 = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-        o1 = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+        o0[k] = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+        o1[k] = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
       }
-      if (ms == ms && ms != -INFINITY) {
-        const float m_new = fmaxf(mx, ms);
+    }
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      if (s0 + k * WPP * SG + g < n_here && ms[k] == ms[k] && ms[k] != -INFINITY) {
+        const float m_new = fmaxf(mx, ms[k]);
         const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
-        const float w = __builtin_amdgcn_exp2f(ms - m_new) * ls;
-        acc0 = acc0 * a_old + w * o0;
-        acc1 = acc1 * a_old + w * o1;
+        const float w = __builtin_amdgcn_exp2f(ms[k] - m_new) * ls[k];
+        acc0 = acc0 * a_old + w * o0[k];
+        acc1 = acc1 * a_old + w * o1[k];
         wsum = wsum * a_old + w;
         mx = m_new;
       }
