@@ -41,7 +41,8 @@ PATCH_CALL = """        from vllm.v1.attention.ops.l20_rocm_fp8_decode import (
 
         if l20_fp8_paged_decode_or_none(self, layer, query, key_cache,
                                         value_cache, output, attn_metadata,
-                                        num_actual_tokens):
+                                        num_actual_tokens,
+                                        output_scale=locals().get("output_scale")):
             return output
 
 """

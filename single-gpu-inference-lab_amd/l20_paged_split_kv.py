@@ -155,13 +155,23 @@ def default_split_size(batch: int, num_kv_heads: int, max_seq_len: int,
     return int(l20_pd_cabi.load().l20_pd_default_split_size(batch, num_kv_heads, max_seq_len, cus))
 
 
-def should_use_l20_paged_fp8_split_kv(batch: int, max_seq_len: int) -> bool:
-    """Dispatch gate used by the vLLM hook.
+def should_use_l20_paged_split_kv(batch: int, max_seq_len: int) -> bool:
+    """Heuristic gate of the 16-bit-cache path: closed, as in the reference
+    (``l20_paged_split_kv.py:698-702``)."""
+    del batch, max_seq_len
+    return False
 
-    The reference keeps its gate closed (``l20_paged_split_kv.py:705-709``)
-    because its L20 kernels lost to FlashInfer in serving.  Here the HIP
-    kernel covers every decode shape the op accepts, so the gate opens for any
-    non-empty decode batch on an MI355X; the hook's
-    ``VLLM_L20_FP8_PAGED_FORCE`` switch still overrides it.
+
+def should_use_l20_paged_fp8_split_kv(batch: int, max_seq_len: int) -> bool:
+    """Heuristic dispatch gate used by the vLLM hook: closed for every shape.
+
+    The reference keeps this gate closed (``l20_paged_split_kv.py:705-709``,
+    asserted by ``tests/test_l20_paged_split_kv_policy.py:26-43``) because its
+    microbenchmark win did not survive a vLLM serving comparison.  No serving
+    comparison of the MI355X kernel against vLLM's own ROCm decode kernel
+    exists (vLLM is not installed where this was built), so the gate stays
+    closed here too; ``VLLM_L20_FP8_PAGED_FORCE=1`` in the hook bypasses it,
+    exactly as in the reference hook (``install_l20_fp8_paged_decode.py:63-90``).
     """
-    return batch > 0 and max_seq_len > 0 and is_mi355x()
+    del batch, max_seq_len
+    return False

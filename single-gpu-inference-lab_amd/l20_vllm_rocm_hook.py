@@ -21,7 +21,8 @@ reference's:
   being captured, the KV cache is fp8 (``float8_e4m3fn`` views) in 16-token
   pages with head_size 64/128, the batch is pure decode (``max_query_len == 1``)
   and the layer uses none of ALiBi, sliding windows, logit soft-capping,
-  attention sinks or a fused output quantisation;
+  attention sinks or a fused output quantisation (``output_scale`` given, or an
+  output buffer whose dtype is not the query's);
 * ``should_use_l20_paged_fp8_split_kv(batch, max_seq_len)`` agrees, unless
   ``VLLM_L20_FP8_PAGED_FORCE=1``;
 * ``VLLM_L20_FP8_PAGED_TRACE=<path>`` appends one JSON line per dispatched call
@@ -35,7 +36,7 @@ from __future__ import annotations
 
 import json
 import os
-from typing import Any
+from typing import Any, Optional
 
 import torch
 
@@ -45,7 +46,7 @@ TRACE_ENV = "VLLM_L20_FP8_PAGED_TRACE"
 SPLIT_SIZE = 512  # the reference hook's split (install_l20_fp8_paged_decode.py:99-121)
 
 
-def _unsupported_features(impl: Any, layer: Any) -> bool:
+def _unsupported_features(impl: Any) -> bool:
     window = getattr(impl, "sliding_window", None)
     if isinstance(window, (tuple, list)):
         window_on = any(w is not None and w >= 0 for w in window)
@@ -56,13 +57,18 @@ def _unsupported_features(impl: Any, layer: Any) -> bool:
         or window_on
         or bool(getattr(impl, "logits_soft_cap", 0) or 0)
         or getattr(impl, "sinks", None) is not None
-        or getattr(layer, "_l20_output_scale", None) is not None
     )
 
 
 def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Tensor,
-                value_cache: torch.Tensor, attn_metadata: Any, num_actual_tokens: int) -> bool:
-    """True when the call may take the MI355X path (all gates but the heuristic)."""
+                value_cache: torch.Tensor, attn_metadata: Any, num_actual_tokens: int,
+                output: Optional[torch.Tensor] = None, output_scale: Any = None) -> bool:
+    """True when the call may take the MI355X path (all gates but the heuristic).
+
+    A fused output quantisation (vLLM passes ``output_scale``, and the output
+    buffer is then fp8) or any output dtype other than the query's is left to
+    vLLM's kernel: the op writes the query dtype only.
+    """
     from l20_paged_split_kv import is_mi355x
 
     if os.getenv(ENABLE_ENV, "0") != "1":
@@ -71,7 +77,13 @@ def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Ten
         return False
     if getattr(attn_metadata, "max_query_len", None) != 1:
         return False
-    if _unsupported_features(impl, layer):
+    if _unsupported_features(impl):
+        return False
+    if output_scale is not None:
+        return False
+    if output is not None and (output.dtype != query.dtype or output.dim() < 2
+                               or output.shape[0] < num_actual_tokens
+                               or output[0].numel() != query[0].numel()):
         return False
     if key_cache.dtype != torch.float8_e4m3fn or value_cache.dtype != torch.float8_e4m3fn:
         return False
@@ -94,10 +106,11 @@ def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Ten
 
 def l20_fp8_paged_decode_or_none(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Tensor,
                                  value_cache: torch.Tensor, output: torch.Tensor, attn_metadata: Any,
-                                 num_actual_tokens: int) -> bool:
+                                 num_actual_tokens: int, output_scale: Any = None) -> bool:
     """Run the decode attention on the MI355X op and return True, or return False
     (and touch nothing) when a gate rejects the call."""
-    if not decode_gate(impl, layer, query, key_cache, value_cache, attn_metadata, num_actual_tokens):
+    if not decode_gate(impl, layer, query, key_cache, value_cache, attn_metadata, num_actual_tokens,
+                       output=output, output_scale=output_scale):
         return False
     from l20_paged_split_kv import (
         allocate_l20_paged_split_kv_workspace,

@@ -232,7 +232,7 @@ def test_hook_api_requires_mi355x_and_fp8_cache():
     with pytest.raises(RuntimeError, match="requires an MI355X"):
         sk.l20_paged_split_kv_attention_fp8(q, kv, kv, torch.zeros(2, 4, dtype=torch.int32),
                                             torch.ones(2, dtype=torch.int32), k_scale=1.0, v_scale=1.0)
-    assert sk.should_use_l20_paged_fp8_split_kv(8, 4096) is False  # no GPU here
+    assert sk.should_use_l20_paged_fp8_split_kv(8, 4096) is False  # closed, as in the reference
 
 
 def test_workspace_allocation_shapes():

@@ -35,6 +35,8 @@ def test_patched_forward_runs_the_op_and_traces(tmp_path, monkeypatch):
     trace = tmp_path / "trace.jsonl"
     monkeypatch.setenv(hook.ENABLE_ENV, "1")
     monkeypatch.setenv(hook.TRACE_ENV, str(trace))
+    # the heuristic gate is closed, as in the reference: FORCE opens the path
+    monkeypatch.setenv(hook.FORCE_ENV, "1")
 
     inp = H.make_synthetic(6, 16, 2, 128, [700, 31, 2048, 1, 300, 999], seed=12)
     kv = torch.stack([inp["key_cache"].view(torch.uint8), inp["value_cache"].view(torch.uint8)])  # [2, P, 16, Hkv, D]
@@ -58,3 +60,15 @@ def test_patched_forward_runs_the_op_and_traces(tmp_path, monkeypatch):
     meta.max_query_len = 4
     impl.forward(layer, q, None, None, kv, meta, output=out)
     assert len(mod.CALLS) == 1
+    # so do a decode batch without FORCE (closed heuristic gate), a fused
+    # output quantisation and an fp8 output buffer
+    meta.max_query_len = 1
+    monkeypatch.delenv(hook.FORCE_ENV)
+    impl.forward(layer, q, None, None, kv, meta, output=out)
+    assert len(mod.CALLS) == 2
+    monkeypatch.setenv(hook.FORCE_ENV, "1")
+    impl.forward(layer, q, None, None, kv, meta, output=out, output_scale=torch.ones((), device="cuda"))
+    assert len(mod.CALLS) == 3
+    impl.forward(layer, q, None, None, kv, meta, output=torch.zeros(8, 16, 128, device="cuda").to(torch.float8_e4m3fn))
+    assert len(mod.CALLS) == 4
+    assert len(trace.read_text().splitlines()) == 2

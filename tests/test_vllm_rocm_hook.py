@@ -124,3 +124,87 @@ def test_patched_forward_falls_back_when_disabled(vllm_tree, monkeypatch):
     out = torch.zeros_like(q)
     impl.forward(layer, q, None, None, kv, meta, output=out)
     assert len(mod.CALLS) == 1 and bool((out == -1).all())
+
+
+def test_heuristic_gates_stay_closed_for_every_shape(monkeypatch):
+    """The reference's policy test (tests/test_l20_paged_split_kv_policy.py:20-43):
+    both heuristic gates are False for every shape, also on an MI355X."""
+    import l20_paged_split_kv
+
+    monkeypatch.setattr(l20_paged_split_kv, "is_mi355x", lambda device=None: True)
+    for batch, max_seq in ((1, 2048), (1, 4096), (4, 4096), (8, 2048), (8, 4096), (128, 8192), (0, 0)):
+        assert l20_paged_split_kv.should_use_l20_paged_fp8_split_kv(batch, max_seq) is False
+        assert l20_paged_split_kv.should_use_l20_paged_split_kv(batch, max_seq) is False
+
+
+def test_dispatch_truth_table(monkeypatch):
+    """ENABLE x FORCE: only ENABLE=1 with FORCE=1 reaches the op (the heuristic gate is closed)."""
+    import l20_paged_split_kv
+
+    monkeypatch.setattr(l20_paged_split_kv, "is_mi355x", lambda device=None: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    ran = []
+    monkeypatch.setattr(l20_paged_split_kv, "l20_paged_split_kv_attention_fp8", lambda *a, **k: ran.append(k))
+    monkeypatch.setattr(l20_paged_split_kv, "allocate_l20_paged_split_kv_workspace", lambda *a, **k: None)
+    impl, layer, q, kc, vc, meta, n = _fake_call()
+    out = torch.zeros_like(q)
+    for enable in ("0", "1"):
+        for force in ("0", "1"):
+            monkeypatch.setenv(hook.ENABLE_ENV, enable)
+            monkeypatch.setenv(hook.FORCE_ENV, force)
+            ran.clear()
+            took = hook.l20_fp8_paged_decode_or_none(impl, layer, q, kc, vc, out, meta, n)
+            assert took == (enable == "1" and force == "1"), (enable, force)
+            assert len(ran) == int(took)
+
+
+def test_gate_rejects_quantised_or_mismatched_output(monkeypatch):
+    import l20_paged_split_kv
+
+    monkeypatch.setattr(l20_paged_split_kv, "is_mi355x", lambda device=None: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setenv(hook.ENABLE_ENV, "1")
+    impl, layer, q, kc, vc, meta, n = _fake_call()
+    assert hook.decode_gate(impl, layer, q, kc, vc, meta, n, output=torch.zeros_like(q))
+    assert hook.decode_gate(impl, layer, q, kc, vc, meta, n, output=torch.zeros(n, 16 * 128, dtype=q.dtype))
+    assert not hook.decode_gate(impl, layer, q, kc, vc, meta, n, output=torch.zeros_like(q),
+                                output_scale=torch.ones(()))
+    assert not hook.decode_gate(impl, layer, q, kc, vc, meta, n,
+                                output=torch.zeros(q.shape, dtype=torch.float8_e4m3fn))
+    assert not hook.decode_gate(impl, layer, q, kc, vc, meta, n, output=torch.zeros(q.shape, dtype=torch.float16))
+    assert not hook.decode_gate(impl, layer, q, kc, vc, meta, n, output=torch.zeros(n - 1, 16, 128, dtype=q.dtype))
+
+
+@pytest.mark.parametrize("case", ["output_scale", "fp8_output"])
+def test_patched_forward_falls_back_on_quantised_output(vllm_tree, monkeypatch, case):
+    """With every env gate open (ENABLE and FORCE) and a GPU stand-in, a fused
+    output quantisation still reaches vLLM's own kernel (the stub)."""
+    import l20_paged_split_kv
+
+    inst.main(["--vllm-source-dir", str(vllm_tree)])
+    monkeypatch.syspath_prepend(str(vllm_tree))
+    monkeypatch.setenv(hook.ENABLE_ENV, "1")
+    monkeypatch.setenv(hook.FORCE_ENV, "1")
+    monkeypatch.setattr(l20_paged_split_kv, "is_mi355x", lambda device=None: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+
+    def must_not_run(*a, **k):
+        raise AssertionError("the MI355X op must not run for a quantised output")
+
+    monkeypatch.setattr(l20_paged_split_kv, "l20_paged_split_kv_attention_fp8", must_not_run)
+    for name in [m for m in sys.modules if m == "vllm" or m.startswith("vllm.")]:
+        monkeypatch.delitem(sys.modules, name)
+    mod = importlib.import_module("vllm.v1.attention.backends.triton_attn")
+    impl = mod.TritonAttentionImpl(16, 128, 128 ** -0.5, 2, kv_cache_dtype="fp8_e4m3")
+    layer = types.SimpleNamespace(_k_scale_float=1.0, _v_scale_float=1.0)
+    kv = torch.zeros(2, 10, 16, 2, 128, dtype=torch.uint8)
+    meta = types.SimpleNamespace(num_actual_tokens=3, query_start_loc=None, seq_lens=torch.ones(3, dtype=torch.int32),
+                                 max_query_len=1, max_seq_len=1, block_table=torch.zeros(3, 1, dtype=torch.int32))
+    q = torch.zeros(3, 16, 128, dtype=torch.bfloat16)
+    if case == "output_scale":
+        out = torch.zeros_like(q)
+        impl.forward(layer, q, None, None, kv, meta, output=out, output_scale=torch.ones(()))
+    else:
+        out = torch.zeros(3, 16, 128, dtype=torch.float8_e4m3fn)
+        impl.forward(layer, q, None, None, kv, meta, output=out)
+    assert len(mod.CALLS) == 1
