@@ -41,6 +41,13 @@ How each function is pinned (tests/test_oracle.py):
   scales vs per-tensor, causal row ``i`` vs a ``q_len = 1`` call on the
   shortened sequence).
 * ``split_reference``: equal to ``reference`` for every split size.
+* ``reference(round_kv_to=np.float16)`` (the reference oracle's literal
+  ``(fp8.float() * scale).to(fp16)`` dequantisation,
+  ``scripts/smoke_cuda_paged_fp8_decode_op.py:23-24``): bit-equal to the fp32
+  path for power-of-two scales (exact in fp16), equal to a torch restatement
+  with torch's own fp16 rounding otherwise, and within the output/LSE
+  tolerances of the fp32 path on every configuration shape.
+* ``reference(acc_dtype=np.float64)``: the float64 brute force to 1e-12.
 """
 
 from __future__ import annotations
@@ -446,13 +453,3 @@ def brute_force_fp64(
                     v = decode[int(value_cache[page, slot, kvh, d])] * float(vs[kvh])
                     out[r, h, d] += w / total * v
     return out, lse
-
-
-def attention_flops(seq_lens: Sequence[int], num_q_heads: int, head_dim: int, q_len: int = 1) -> int:
-    """``4 * Hq * q * D * sum(L)`` (QK and PV, two FLOPs per FMA)."""
-    return int(4 * num_q_heads * q_len * head_dim * int(np.sum(seq_lens)))
-
-
-def kv_bytes(seq_lens: Sequence[int], num_kv_heads: int, head_dim: int) -> int:
-    """Algorithmic FP8 K+V bytes read per call: ``sum(L) * Hkv * D * 2``."""
-    return int(np.sum(np.asarray(seq_lens, dtype=np.int64)) * num_kv_heads * head_dim * 2)

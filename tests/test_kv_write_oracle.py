@@ -37,6 +37,17 @@ def _complex_rope(x, theta, is_neox, rot):
     return out
 
 
+@pytest.mark.parametrize("dtype,torch_dtype", [("bf16", torch.bfloat16), ("fp16", torch.float16)])
+def test_round_to_matches_torch_casts(dtype, torch_dtype):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(4000) * 100, rng.standard_normal(4000) * 1e-6,
+                        [0.0, -0.0, 65504.0, 1e-8]]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch_dtype).float().numpy()
+    assert np.array_equal(kw.round_to(x, dtype), want)
+    with pytest.raises(ValueError):
+        kw.round_to(x, "fp8")
+
+
 @pytest.mark.parametrize("is_neox", [True, False])
 @pytest.mark.parametrize("rot,d", [(128, 128), (64, 128), (32, 64)])
 def test_rope_matches_complex_rotation(is_neox, rot, d):

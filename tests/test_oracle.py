@@ -409,3 +409,109 @@ def test_tree_reference_matches_brute_force(seed):
     # a planted mistake (bits shifted by one draft position) is caught
     bad = run(ref.reference, case, tree_mask=bits << 1)
     assert not np.allclose(bad[0], want[0], atol=1e-3)
+
+
+# ---------------------------------------------------------------- literal fp16 dequantisation
+# The reference oracle rounds the dequantised K/V to fp16 before attending
+# (scripts/smoke_cuda_paged_fp8_decode_op.py:23-24); this oracle keeps fp32.
+def _power_of_two_case():
+    case = make_case(seed=21, batch=2, hq=4, hkv=2, d=64, lens=[37, 70], q_len=2)
+    return dict(case, k_scale=0.125, v_scale=2.0 ** -5)
+
+
+@pytest.mark.parametrize("spec", TINY)
+def test_acc_f64_is_closer_to_brute_force_than_acc_f32(spec):
+    """float64 accumulation (outputs still stored as float32, K/V dequantised
+    in float32 as the reference does) lands nearer the float64 loop than the
+    float32 path does; an ignored ``acc_dtype`` would tie."""
+    case = make_case(**spec)
+    out32, _ = run(ref.reference, case)
+    out64, lse64 = run(ref.reference, case, acc_dtype=np.float64)
+    want, want_lse = run(ref.brute_force_fp64, case)
+    err64 = np.abs(out64 - want).max()
+    assert err64 <= 1.5e-7 and err64 <= 0.6 * np.abs(out32 - want).max()
+    np.testing.assert_allclose(lse64, want_lse, atol=5e-7, rtol=0)
+
+
+def test_f16_dequant_is_exact_for_power_of_two_scales():
+    """Every e4m3fn value times 2^-k (k small) is an fp16 value, so the
+    fp16-rounded path must equal the fp32 path bit for bit."""
+    case = _power_of_two_case()
+    out32, lse32 = run(ref.reference, case)
+    out16, lse16 = run(ref.reference, case, round_kv_to=np.float16)
+    assert np.array_equal(out16, out32) and np.array_equal(lse16, lse32)
+
+
+def _torch_literal_reference(case):
+    """The reference oracle's steps in torch (fp8 -> float -> * scale -> fp16,
+    gather, GQA repeat, softmax, weighted V), causal over the newest q_len."""
+    q_len = case["q_len"]
+    query = torch.from_numpy(case["query"])
+    kc = torch.from_numpy(case["key_cache"]).view(torch.float8_e4m3fn)
+    vc = torch.from_numpy(case["value_cache"]).view(torch.float8_e4m3fn)
+    hq, d = query.shape[1], query.shape[2]
+    hkv = kc.shape[2]
+    outs = []
+    for b, length in enumerate(case["seq_lens"].tolist()):
+        t = torch.arange(length)
+        pages = torch.from_numpy(case["block_table"][b]).long()[t // 16]
+        k = (kc[pages, t % 16].float() * float(case["k_scale"])).to(torch.float16).float()
+        v = (vc[pages, t % 16].float() * float(case["v_scale"])).to(torch.float16).float()
+        k = k.repeat_interleave(hq // hkv, dim=1)
+        v = v.repeat_interleave(hq // hkv, dim=1)
+        for i in range(q_len):
+            lim = length - q_len + i + 1
+            s = torch.einsum("hd,thd->ht", query[b * q_len + i], k[:lim]) * d ** -0.5
+            outs.append(torch.einsum("ht,thd->hd", torch.softmax(s, dim=-1), v[:lim]))
+    return torch.stack(outs).numpy()
+
+
+def test_f16_dequant_matches_torch_literal_restatement():
+    """Non-power-of-two scales: the fp16 rounding changes the result, and the
+    oracle's rounded path matches torch's own fp16 cast of the same products.
+    A rounding applied before the scale (exact, so a no-op) or to bf16 fails."""
+    case = make_case(seed=22, batch=2, hq=6, hkv=2, d=128, lens=[50, 93], q_len=2)
+    out32, _ = run(ref.reference, case)
+    out16, _ = run(ref.reference, case, round_kv_to=np.float16)
+    want = _torch_literal_reference(case)
+    assert np.abs(out16 - out32).max() > 1e-6
+    np.testing.assert_allclose(out16, want, atol=2e-6, rtol=0)
+    assert np.abs(out32 - want).max() > 4 * np.abs(out16 - want).max()
+
+
+def _reduced(name):
+    """The configuration's head layout, scales and q_len on a few sequences."""
+    import dataclasses
+
+    import l20_pd_workloads as wl
+
+    kw = {"c2_qwen2.5_coder_3b": dict(batch=4), "c3_qwen2.5_7b": dict(batch=16),
+          "c4_llama3_8b_long": dict(batch=1, context=16384), "c5_llama3_70b_verify": dict(batch=3)}
+    return dataclasses.replace(wl.CONFIGS[name], **kw.get(name, {}))
+
+
+@pytest.mark.parametrize("name", ["c1_qwen2.5_0.5b", "c2_qwen2.5_coder_3b", "c3_qwen2.5_7b",
+                                  "c4_llama3_8b_long", "c5_llama3_70b_verify"])
+def test_reference_literal_f16_dequant_within_tolerance_of_fp32_oracle(name):
+    """The reference's literal oracle and this fp32 oracle agree within the
+    north-star tolerances (max-abs 1e-2, cosine 0.9999, LSE 1e-4 relative) on
+    every configuration shape, so parity against either is the same claim."""
+    import l20_pd_workloads as wl
+
+    cfg = _reduced(name)
+    inp = wl.make_inputs(cfg)
+
+    def sc(x):
+        return x if isinstance(x, float) else x.numpy()
+
+    args = (inp["query"].float().numpy(), inp["key_cache"].view(torch.uint8).numpy(),
+            inp["value_cache"].view(torch.uint8).numpy(), inp["block_table"].numpy(), inp["seq_lens"].numpy(),
+            sc(inp["k_scale"]), sc(inp["v_scale"]))
+    o32, l32 = ref.reference(*args, softmax_scale=inp["softmax_scale"], q_len=cfg.q_len)
+    o16, l16 = ref.reference(*args, softmax_scale=inp["softmax_scale"], q_len=cfg.q_len, round_kv_to=np.float16)
+    a = o32.reshape(-1, o32.shape[-1]).astype(np.float64)
+    b = o16.reshape(-1, o16.shape[-1]).astype(np.float64)
+    cos = (a * b).sum(-1) / np.maximum(np.linalg.norm(a, axis=-1) * np.linalg.norm(b, axis=-1), 1e-30)
+    assert np.abs(o32 - o16).max() <= 1e-2 / 10
+    assert cos.min() >= 0.9999
+    assert (np.abs(l32 - l16) / np.maximum(1.0, np.abs(l32))).max() <= 1e-4
