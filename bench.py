@@ -12,8 +12,9 @@ Prints ONE JSON line (rank 0): value = KV-read GB/s of the whole call
 between two events), plus the partial kernel's roofline (algorithmic KV
 bytes / its own mean duration from HIP events recorded around it on the
 launch stream, in a second timed loop: an event between the two kernels adds
-a packet to the call) and a CPU baseline: the CPU oracle timed on this host
-over a bounded sample of the same workload.
+a packet to the call) and a CPU baseline: a torch CPU restatement of the reference's
+oracle timed on this host's usable cores over a bounded sample of the same
+workload.
 
 ``--workload`` measures the other parts of the path the same way (the
 default, ``decode``, is the headline):
@@ -71,12 +72,15 @@ def parse():
     return ap.parse_args()
 
 
-def threads_in_use():
-    try:
-        from threadpoolctl import threadpool_info
-        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover - threadpoolctl is optional
-        return 1
+def cpu_threads():
+    """Threads for the CPU baseline: the host CPUs this process may run on
+    (``sched_getaffinity``), capped by ``OMP_NUM_THREADS`` when the host sets
+    it (the GPU box gives one GPU's job a CPU share through it).  Returns
+    ``(threads, cpus_visible)``."""
+    visible = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(visible, int(omp)) if omp.isdigit() and int(omp) > 0 else visible
+    return threads, visible
 
 
 def sample_inputs(inp, rows):
@@ -126,26 +130,69 @@ def oracle_call(inp, rows):
     return res, int(sl.sum()), kc.shape, time.perf_counter() - t0
 
 
-def cpu_baseline_decode(inp, cfg, sample_seqs, elem_bytes, min_seconds=10.0):
-    """Time the CPU oracle over the first ``sample_seqs`` sequences of one input
-    set: at least three calls, repeated until ``min_seconds`` of CPU work (at
-    most 50 calls); the median call gives the rate."""
-    import l20_pd_workloads as wl
+def sample_inputs_torch(inp, rows):
+    """CPU torch copies of the sequences ``rows`` of an input set (caches keep
+    their dtype), pages renumbered into a compact pool."""
+    import torch
 
-    rows = list(range(sample_seqs))
+    bt = inp["block_table"].cpu()
+    sl = inp["seq_lens"].cpu()
+    q_len = inp["q_len"]
+    pages, table = [], torch.zeros((len(rows), bt.shape[1]), dtype=torch.int32)
+    for i, b in enumerate(rows):
+        n = (int(sl[b]) + 15) // 16
+        table[i, :n] = torch.arange(len(pages), len(pages) + n, dtype=torch.int32)
+        pages.extend(bt[b, :n].tolist())
+    idx = torch.as_tensor(pages, dtype=torch.long, device=inp["key_cache"].device)
+    q = inp["query"].cpu().view(-1, q_len, *inp["query"].shape[1:])[rows].reshape(-1, *inp["query"].shape[1:])
+    tree = inp.get("tree_mask")
+
+    def sc(x):
+        return x if isinstance(x, float) else x.float().cpu()
+
+    return {"query": q, "key_cache": inp["key_cache"].index_select(0, idx).cpu(),
+            "value_cache": inp["value_cache"].index_select(0, idx).cpu(), "block_table": table,
+            "seq_lens": sl[rows], "k_scale": sc(inp["k_scale"]), "v_scale": sc(inp["v_scale"]),
+            "tree_mask": None if tree is None else tree.cpu()[rows]}
+
+
+def cpu_baseline_decode(inp, cfg, sample_seqs, elem_bytes, min_seconds=10.0):
+    """Time the torch CPU restatement of the reference's oracle over the first
+    ``sample_seqs`` sequences of one input set, with one thread per usable host
+    CPU: at least three calls, repeated until ``min_seconds`` of CPU work (at
+    most 50 calls); the median call gives the rate."""
+    import torch
+
+    import l20_pd_workloads as wl
+    from oracle import paged_fp8_decode_torch as tref
+
+    threads, visible = cpu_threads()
+    before = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    s = sample_inputs_torch(inp, list(range(sample_seqs)))
     times = []
-    while len(times) < 3 or (sum(times) < min_seconds and len(times) < 50):
-        times.append(oracle_call(inp, rows)[3])
+    try:
+        while len(times) < 3 or (sum(times) < min_seconds and len(times) < 50):
+            t0 = time.perf_counter()
+            tref.reference_torch(s["query"], s["key_cache"], s["value_cache"], s["block_table"], s["seq_lens"],
+                                 s["k_scale"], s["v_scale"], softmax_scale=inp["softmax_scale"], q_len=inp["q_len"],
+                                 tree_mask=s["tree_mask"])
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(before)
     t = statistics.median(times)
-    sl = inp["seq_lens"][:sample_seqs].cpu()
+    sl = s["seq_lens"]
     kv = wl.kv_bytes(sl, cfg.num_kv_heads, cfg.head_dim, elem_bytes)
     return {
         "value": round(kv / t / 1e9, 3),
         "unit": "GB/s",
-        "cores": int(threads_in_use()),
+        "cores": int(threads),
+        "host_cpus_visible": int(visible),
         "kind": "port",
-        "sample": f"numpy oracle (oracle/paged_fp8_decode_ref.py) over sequences 0..{sample_seqs - 1} of the "
-                  f"workload ({int(sl.sum())} tokens, {kv / 1e6:.1f} MB KV), median of {len(times)} calls "
+        "sample": f"torch CPU restatement of the reference's dequantise-then-attend oracle "
+                  f"(scripts/smoke_cuda_paged_fp8_decode_op.py:22-41; oracle/paged_fp8_decode_torch.py, fp32, "
+                  f"torch.set_num_threads({threads})) over sequences 0..{sample_seqs - 1} of the workload "
+                  f"({int(sl.sum())} tokens, {kv / 1e6:.1f} MB KV), median of {len(times)} calls "
                   f"({sum(times):.1f} s of CPU work), {t * 1e3:.1f} ms per sample call",
         "us_per_call_sample": round(t * 1e6, 1),
     }
@@ -494,9 +541,10 @@ def run_kv_write(args):
             times.append(oracle_sample(n)[1])
         t = statistics.median(times)
         sample_bytes = kv_write_bytes(dict(c, tokens=n))
-        cpu = {"value": round(sample_bytes / t / 1e9, 4), "unit": "GB/s", "cores": int(threads_in_use()),
-               "kind": "port",
-               "sample": f"numpy oracle (oracle/kv_write_ref.py) over the first {n} tokens of the chunk "
+        cpu = {"value": round(sample_bytes / t / 1e9, 4), "unit": "GB/s", "cores": 1,
+               "host_cpus_visible": int(cpu_threads()[1]), "kind": "port",
+               "sample": f"numpy oracle (oracle/kv_write_ref.py; elementwise numpy, one thread) over the first "
+                         f"{n} tokens of the chunk "
                          f"({sample_bytes / 1e6:.1f} MB of algorithmic traffic), median of {len(times)} calls "
                          f"({sum(times):.1f} s of CPU work), {t * 1e3:.1f} ms per sample call"}
 

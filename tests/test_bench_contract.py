@@ -51,3 +51,24 @@ def test_headline_line_carries_every_contract_field():
     assert r0["traffic"] is None or r0["traffic"] > d["config"]["kv_bytes_per_call"]
     assert d["cpu_baseline"] is None  # disabled by the flag
     assert d["parity"]["min_cos"] >= 0.9999
+
+
+def test_cpu_baseline_fields_on_the_cpu(monkeypatch):
+    """The CPU baseline times the torch restatement with one thread per usable
+    host CPU (capped by OMP_NUM_THREADS) and reports that count as ``cores``."""
+    import os
+    import types
+
+    import pd_helpers as H
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    monkeypatch.setenv("OMP_NUM_THREADS", "2")
+    inp = H.make_synthetic(3, 8, 2, 64, [40, 17, 90], seed=4, device="cpu")
+    cfg = types.SimpleNamespace(num_kv_heads=2, head_dim=64)
+    cpu = bench.cpu_baseline_decode(inp, cfg, 2, 1, min_seconds=0.01)
+    assert cpu["kind"] == "port" and cpu["unit"] == "GB/s" and cpu["value"] > 0
+    assert cpu["cores"] == min(2, len(os.sched_getaffinity(0)))
+    assert cpu["host_cpus_visible"] == len(os.sched_getaffinity(0))
+    assert "torch CPU restatement" in cpu["sample"] and "57 tokens" in cpu["sample"]
