@@ -157,6 +157,20 @@ int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args);
  * calls use different work-queue counters, 64 of them per device. */
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
 
+/* Allocation-free variant of l20_pd_fp8_e4m3_split_out (no counterpart in the
+ * reference: for callers that cannot allocate device memory, such as code
+ * under HIP graph capture, tight serving loops or harnesses that forbid
+ * hipMalloc).  Same arguments and kernels, but the partial_* fields of `args`
+ * are ignored: the fp32 split partials go to a 64 MiB array the library holds
+ * on each device for the life of the process (its address is looked up once
+ * per device, on the first call with that device current).  Calls needing more
+ * than 64 MiB of partials (batch*q_len*num_q_heads*ceil(max_seq_len/split_size)
+ * *(head_dim+2)*4 bytes) return L20_PD_EINVAL.  The caller passes the inputs,
+ * output and (optionally) lse; nothing is allocated.  Every call on a device
+ * shares that device's array, so calls that overlap on one device (different
+ * streams, or host threads) race and must be serialised by the caller. */
+int32_t l20_pd_fp8_e4m3_split_out_noalloc(const l20_pd_fp8_args *args, void *stream);
+
 /* The fp16/bf16-KV sibling: the same two kernels over 16-bit caches
  * (kv_dtype L20_PD_KV_FP16 or L20_PD_KV_BF16, query of the same type; the
  * scalar/per-head scales still multiply K and V, 1.0 reproduces the

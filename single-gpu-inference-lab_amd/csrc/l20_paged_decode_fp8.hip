@@ -42,6 +42,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "l20_paged_decode.h"
@@ -1786,6 +1787,47 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   return L20_PD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Library-held scratch for the allocation-free entry point
+// ---------------------------------------------------------------------------
+// The split partials (o / l, m, l) of l20_pd_fp8_e4m3_split_out_noalloc live
+// in this array instead of a caller workspace.  Each device the library runs
+// on holds its own copy for the life of the process.  Host code never passes
+// the array's name to a kernel or a copy (on the host it is only a stand-in
+// for the symbol): the device address comes from hipGetSymbolAddress, looked
+// up once per device with that device current, and kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array (nullptr after a
+// failed lookup, with the error recorded).
+void *scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(L20_PD_ELAUNCH, "noalloc: no current HIP device (or device index >= 64)");
+    return nullptr;
+  }
+  void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (p) return p;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    snprintf(g_last_error, sizeof(g_last_error), "noalloc: hipGetSymbolAddress(scratch) failed: %s",
+             hipGetErrorString(e));
+    return nullptr;
+  }
+  g_scratch_ptr[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 }  // namespace
 
 // Error reporting for the other translation units of the library.
@@ -1833,6 +1875,48 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
 }
 
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth, kKvFp8); }
+
+int32_t l20_pd_fp8_e4m3_split_out_noalloc(const l20_pd_fp8_args *a, void *stream) {
+  g_last_error[0] = '\0';
+  if (!a) return fail(L20_PD_EINVAL, "null argument block");
+  l20_pd_fp8_args c = *a;
+  c.partial_output = nullptr;
+  c.partial_max = nullptr;
+  c.partial_sum = nullptr;
+  c.partial_splits = 0;
+  const int32_t n_s = l20_pd_num_splits(c.max_seq_len, c.split_size);
+  // Shapes the checks reject anyway need no scratch; run() reports them.
+  const bool sane = c.batch > 0 && c.q_len >= 1 && c.num_q_heads > 0 && (c.head_dim == 64 || c.head_dim == 128);
+  if (n_s > 1 && sane) {
+    // fp32 partials [rows, Hq, n_s, D] then m and l [rows, Hq, n_s], each 256-byte aligned
+    const double pairs = (double)c.batch * c.q_len * c.num_q_heads * n_s;
+    if (pairs * (c.head_dim + 2) * 4.0 + 768.0 > (double)kScratchBytes) {
+      char msg[256];
+      snprintf(msg, sizeof(msg),
+               "noalloc: the split partials need %.0f bytes, more than the %zu-byte scratch; use "
+               "l20_pd_fp8_e4m3_split_out with a workspace",
+               pairs * (c.head_dim + 2) * 4.0, kScratchBytes);
+      return fail(L20_PD_EINVAL, msg);
+    }
+    unsigned char *base = static_cast<unsigned char *>(scratch_ptr());
+    if (!base) return L20_PD_ELAUNCH;
+    const size_t np = (size_t)pairs;
+    const size_t o_bytes = align256(np * (size_t)c.head_dim * 4);
+    const size_t ml_bytes = align256(np * 4);
+    c.partial_output = base;
+    c.partial_dtype = L20_PD_FP32;
+    c.po_stride_split = c.head_dim;
+    c.po_stride_head = (int64_t)n_s * c.head_dim;
+    c.po_stride_row = (int64_t)c.num_q_heads * n_s * c.head_dim;
+    c.partial_splits = n_s;
+    c.partial_max = reinterpret_cast<float *>(base + o_bytes);
+    c.partial_sum = reinterpret_cast<float *>(base + o_bytes + ml_bytes);
+    c.pm_stride_split = c.ps_stride_split = 1;
+    c.pm_stride_head = c.ps_stride_head = n_s;
+    c.pm_stride_row = c.ps_stride_row = (int64_t)c.num_q_heads * n_s;
+  }
+  return run(&c, stream, kBoth, kKvFp8);
+}
 
 int32_t l20_pd_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth, kKv16); }
 

@@ -26,6 +26,7 @@ EXPORTED = (
     "l20_pd_num_splits",
     "l20_pd_fp8_e4m3_check",
     "l20_pd_fp8_e4m3_split_out",
+    "l20_pd_fp8_e4m3_split_out_noalloc",
     "l20_pd_split_out",
     "l20_pd_fp8_e4m3_partial",
     "l20_pd_fp8_e4m3_merge",
@@ -105,8 +106,8 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     args_p = ctypes.POINTER(L20PdFp8Args)
     lib.l20_pd_fp8_e4m3_check.argtypes = [args_p]
     lib.l20_pd_fp8_e4m3_check.restype = _i32
-    for name in ("l20_pd_fp8_e4m3_split_out", "l20_pd_split_out", "l20_pd_fp8_e4m3_partial",
-                 "l20_pd_fp8_e4m3_merge"):
+    for name in ("l20_pd_fp8_e4m3_split_out", "l20_pd_fp8_e4m3_split_out_noalloc", "l20_pd_split_out",
+                 "l20_pd_fp8_e4m3_partial", "l20_pd_fp8_e4m3_merge"):
         getattr(lib, name).argtypes = [args_p, _vp]
         getattr(lib, name).restype = _i32
     lib.l20_pd_default_split_size.argtypes = [_i32, _i32, _i32, _i32]
@@ -225,6 +226,12 @@ def split_out(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = 
     caches); raise RuntimeError with the library's message on failure."""
     name = "l20_pd_fp8_e4m3_split_out" if args.kv_dtype == L20_PD_KV_FP8_E4M3 else "l20_pd_split_out"
     _call(name, args, stream, lib)
+
+
+def split_out_noalloc(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
+    """Call ``l20_pd_fp8_e4m3_split_out_noalloc``: the split partials go to the
+    library's own per-device scratch (the struct's partial_* fields are ignored)."""
+    _call("l20_pd_fp8_e4m3_split_out_noalloc", args, stream, lib)
 
 
 def partial(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
