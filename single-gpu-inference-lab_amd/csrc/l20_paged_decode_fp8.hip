@@ -43,6 +43,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <vector>
 #include <type_traits>
 
 #include "l20_paged_decode.h"
@@ -270,6 +271,406 @@ __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 
 constexpr int kQueueSlots = 64;
 __device__ __align__(64) unsigned int g_pd_queue[kQueueSlots][16];
 
+// ---------------------------------------------------------------------------
+// Per-unit math of the partial kernel
+// ---------------------------------------------------------------------------
+// A unit is one wave's scan of one KV head over a token range of one
+// sequence.  Lane layout: n16 = lane % 16 is query column 16*qt + n16 of the
+// MFMA tile (G x q_len query rows, padded to 16 * NQT), j = lane / 16.
+// Blocks hold 32 fp8 tokens (two 16-token pages: tiles 2*blk, 2*blk + 1 of
+// the unit's page-id window) or 16 tokens of a 16-bit cache (tile blk).
+template <typename QT, int KT, int D, int NQT, bool TREE>
+struct KvUnit {
+  typedef typename MfmaTypes<QT>::vec8 qvec8;
+  typedef typename KvBlock<KT, D>::type Block;
+  // Softmax probabilities: f16 for fp8 caches (V converted to f16), the
+  // cache's own type for 16-bit caches.
+  typedef typename std::conditional<KT == 0, _Float16, QT>::type PT;
+  typedef typename MfmaTypes<PT>::vec8 pvec8;
+  static constexpr int kTok = KT == 0 ? 32 : 16;  // tokens per block
+  // bf16 probabilities carry 8 significant bits: split P = hi + lo (both
+  // bf16) and accumulate both products, which restores ~16 bits.
+  static constexpr bool kSplitP = KT == 1 && std::is_same<QT, __bf16>::value;
+  static constexpr int NCH = D / 64;  // 64-byte K chunks per token row
+  static constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
+  static constexpr int NT = D / 16;   // 16-row d tiles of the PV product
+  static constexpr int DPL = D / 4;   // contiguous output dims per lane
+
+  // online-softmax state: O^T tiles, running max (log2 units) and sum per column
+  f32x4 acc[NQT][NT];
+  float m_run[NQT], l_run[NQT];
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      m_run[qt] = -INFINITY;
+      l_run[qt] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  // Raw buffer loads through a per-page resource: the page base lives in
+  // SGPRs, one 32-bit lane offset serves every K (V) load of the page and the
+  // hardware range check (the page's byte extent) returns zeros for anything
+  // outside it.  Loads are unconditional -- an invalid page id reads page 0 --
+  // and compute_block zeroes V of every token outside the unit or on an
+  // invalid page.  Lane offsets inside a page fit in 32 bits (checked on the
+  // host).  parts: 1 = the K loads, 2 = the V loads, 3 = both.
+  static __device__ __forceinline__ void load_block(const PartialParams &p, Block &r, int pid, int kvh, int blk,
+                                                    int parts, int n16, int j) {
+    if constexpr (KT == 1) {
+      // 16-bit elements: one page per block; K slice s at byte 128*(s/2) + 16*(s%2)
+      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 32 * j);
+      const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + 2 * (D / 16) * n16);
+      const int raw_page = __builtin_amdgcn_readlane(pid, blk);
+      const int page = raw_page >= 0 ? raw_page : 0;
+      if (parts & 1) {
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          r.k[s] = __builtin_bit_cast(
+              i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), kStreamPolicy));
+      }
+      if (parts & 2) {
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (D == 128)
+            r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, kStreamPolicy));
+          else
+            r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
+        }
+      }
+    } else {
+      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
+      const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
+        const int page = raw_page >= 0 ? raw_page : 0;
+        if (parts & 1) {
+          const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, kStreamPolicy));
+        }
+        if (parts & 2) {
+          const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (D == 128)
+              r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
+            else
+              r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, kStreamPolicy);
+          }
+        }
+      }
+    }
+  }
+
+  // Query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16.
+  static __device__ __forceinline__ void load_q(const PartialParams &p, int b, int kvh, qvec8 (&dst)[NQT][NS], int n16,
+                                                int j) {
+    const int q_len = p.q_len;
+    const int mcols = p.group * q_len;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const int col = 16 * qt + n16;
+      const int g = col / q_len;
+      const int i = col - g * q_len;
+      if (col < mcols) {
+        const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
+                         (int64_t)(kvh * p.group + g) * p.q_shead;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
+          dst[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dst[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
+      }
+    }
+  }
+
+  // Tree verification: ancestor words of this lane's query columns over the
+  // newest q_len keys (bit j lets the column see key L - q_len + j).  The
+  // causal rule (TREE = false) keeps no words: its limit is recomputed per
+  // unit, which keeps the tree state out of the causal kernels' registers.
+  static __device__ __forceinline__ void load_tree(const PartialParams &p, int b, int (&dst)[TREE ? NQT : 1], int n16) {
+    if constexpr (TREE) {
+      const int mcols = p.group * p.q_len;
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        const int col = 16 * qt + n16;
+        dst[qt] = col < mcols ? p.tree[(int64_t)b * p.tree_sb + (col % p.q_len)] : 0;
+      }
+    }
+  }
+
+  // One block: tokens tok0 .. tok0 + kTok - 1 of the sequence, page ids in
+  // lanes kTilesPerBlock*blk (+1) of pid.  Keys at or past uEnd, on an
+  // invalid page, or hidden by the mask get score -inf and zero V.  Keys
+  // before draft0 are visible to every column; key draft0 + j to draft row i
+  // when j <= i (causal: lim is the lane column's last visible key) or when
+  // bit j of the row's ancestor word is set (TREE); min_lim is the last key
+  // every column sees.  after_scores() runs once r.k has been consumed.
+  template <typename F>
+  __device__ __forceinline__ void compute_block(Block &r, int pid, int blk, int tok0, int uEnd, int draft0,
+                                                const int (&lim)[TREE ? 1 : NQT], int min_lim,
+                                                const int (&tree)[TREE ? NQT : 1], const qvec8 (&qop)[NQT][NS],
+                                                float c_log2, int j, F &&after_scores) {
+    // Tokens past the unit (the tail of the sequence's last page, or a tile
+    // beyond the unit read from page 0) and tokens of an invalid page may hold
+    // arbitrary bytes, NaN codes included: zero their V so that p = 0
+    // contributes exactly 0.  K needs no fix-up: their scores are replaced by
+    // -inf below.  A 16-bit block has one tile; its second-tile slots are
+    // empty (score -inf, V zero).
+    const bool bad0 = __builtin_amdgcn_readlane(pid, KT == 0 ? 2 * blk : blk) < 0;
+    const bool bad1 = KT == 0 ? __builtin_amdgcn_readlane(pid, 2 * blk + 1) < 0 : true;
+    if constexpr (KT == 0) {
+      if (tok0 + 32 > uEnd || bad0 || bad1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+          if (t >= uEnd || ((e >> 2) ? bad1 : bad0)) {
+            if constexpr (D == 128)
+              r.v[e] = i32x2{0, 0};
+            else
+              r.v[e] = 0;
+          }
+        }
+      }
+    } else {
+      if (tok0 + 16 > uEnd || bad0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (tok0 + 4 * j + e >= uEnd || bad0) {
+            if constexpr (D == 128)
+              r.v[e] = i32x4{0, 0, 0, 0};
+            else
+              r.v[e] = i32x2{0, 0};
+          }
+        }
+      }
+    }
+    // ---- S^T = K . Q^T ----
+    f32x4 sc[NQT][2];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if constexpr (KT == 0) {
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const i32x4 raw = r.k[T][s >> 1];
+          const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
+#pragma unroll
+          for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const qvec8 kop = __builtin_bit_cast(qvec8, r.k[s]);
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) sc[qt][0] = mfma16(kop, qop[qt][s], sc[qt][0]);
+      }
+    }
+    // r.k is consumed: the refill's K loads may overwrite it
+    after_scores();
+    // ---- online softmax (log2 domain) ----
+    const bool need_mask = (tok0 + kTok - 1 > min_lim) || bad0 || bad1;
+    pvec8 pop[NQT];
+    pvec8 pop_lo[kSplitP ? NQT : 1];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = sc[qt][e >> 2][e & 3] * c_log2;
+      if (need_mask) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
+          bool vis;
+          if constexpr (TREE)
+            vis = t < uEnd && (t < draft0 || (((uint32_t)tree[qt] >> ((t - draft0) & 31)) & 1u));
+          else
+            vis = t <= lim[qt];
+          x[e] = (vis && !((e >> 2) ? bad1 : bad0)) ? x[e] : -INFINITY;
+        }
+      }
+      float mloc = x[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
+      mloc = wave_max_xor16_32(mloc);
+      // Lazy rescale: the reference max m_run only moves when some column's
+      // block max exceeds it by more than kRescaleLog2 (or it is still -inf).
+      // P and l always use the same m_run, so the result is exact up to
+      // rounding; p stays below 2^kRescaleLog2 (f16 range).
+      if (__any(mloc > m_run[qt] + kRescaleLog2)) {
+        const float m_new = fmaxf(m_run[qt], mloc);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
+        l_run[qt] *= alpha;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[qt][t] *= alpha;
+        m_run[qt] = m_new;
+      }
+      const float m_use = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
+      float psum = 0.0f;
+      i32x4 pw, pw_lo;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(x[e] - m_use);
+        const float p1 = __builtin_amdgcn_exp2f(x[e + 1] - m_use);
+        psum += p0 + p1;
+        pw[e >> 1] = pack2<PT>(p0, p1);
+        if constexpr (kSplitP) {
+          // bf16 -> f32 is exact: the halves are the top 16 bits of an f32
+          const uint32_t w = (uint32_t)pw[e >> 1];
+          pw_lo[e >> 1] = pack2<PT>(p0 - __builtin_bit_cast(float, w << 16), p1 - __builtin_bit_cast(float, w & 0xffff0000u));
+        }
+      }
+      pop[qt] = __builtin_bit_cast(pvec8, pw);
+      if constexpr (kSplitP) pop_lo[qt] = __builtin_bit_cast(pvec8, pw_lo);
+      l_run[qt] += psum;
+    }
+    // ---- O^T += V^T . P^T ----
+    // d tile t (0 <= t < D/16) holds dims 8*(lane%16) + t (D = 128) or
+    // 4*(lane%16) + t (D = 64); k slot i of the V^T and P^T operands is
+    // token 16*(i/4) + 4*(lane/16) + i%4 of the block.
+#pragma unroll
+    for (int tp2 = 0; tp2 < NT; tp2 += 2) {
+      i32x4 wa, wb;
+      if constexpr (KT == 0) {
+        // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          int w0, w1;
+          if constexpr (D == 128) {
+            w0 = r.v[e][tp2 >> 2];
+            w1 = r.v[e + 1][tp2 >> 2];
+          } else {
+            w0 = r.v[e];
+            w1 = r.v[e + 1];
+          }
+          const f32x2 f0 = fp8x2_f32(w0, (tp2 & 3) != 0);
+          const f32x2 f1 = fp8x2_f32(w1, (tp2 & 3) != 0);
+          wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
+          wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
+        }
+      } else {
+        // d tiles tp2, tp2+1 are the low and high halves of dword tp2 / 2:
+        // pair the halves of tokens (0, 1) and (2, 3); slots 4-7 are empty
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const uint32_t w0 = (uint32_t)r.v[e][tp2 >> 1];
+          const uint32_t w1 = (uint32_t)r.v[e + 1][tp2 >> 1];
+          wa[e >> 1] = (int)((w0 & 0xffffu) | (w1 << 16));
+          wb[e >> 1] = (int)((w0 >> 16) | (w1 & 0xffff0000u));
+        }
+        wa[2] = wa[3] = 0;
+        wb[2] = wb[3] = 0;
+      }
+      const pvec8 va = __builtin_bit_cast(pvec8, wa);
+      const pvec8 vb = __builtin_bit_cast(pvec8, wb);
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        acc[qt][tp2] = mfma16(va, pop[qt], acc[qt][tp2]);
+        acc[qt][tp2 + 1] = mfma16(vb, pop[qt], acc[qt][tp2 + 1]);
+        if constexpr (kSplitP) {
+          acc[qt][tp2] = mfma16(va, pop_lo[qt], acc[qt][tp2]);
+          acc[qt][tp2 + 1] = mfma16(vb, pop_lo[qt], acc[qt][tp2 + 1]);
+        }
+      }
+    }
+  }
+
+  // Epilogue: this lane holds column 16*qt + lane%16, dims [DPL*j, DPL*j + DPL).
+  // direct: the unit covered the whole sequence; write the output and the
+  // LSE (and, with a workspace, mark split slot 0 of the row +inf for the
+  // merge).  Otherwise write the fp32 (or fp16) partial (O / l, m, l) of query
+  // row i at workspace row slot_row * q_len + i, split slot_split.
+  __device__ __forceinline__ void finish(const PartialParams &p, int b, int kvh, bool direct, int64_t slot_row,
+                                         int64_t slot_split, bool mark_final, float v_scale, int n16, int j) {
+    const int q_len = p.q_len;
+    const int mcols = p.group * q_len;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const float l_tot = wave_sum_xor16_32(l_run[qt]);
+      const int col = 16 * qt + n16;
+      if (col >= mcols) continue;
+      const float inv = (l_tot > 0.0f) ? v_scale / l_tot : 0.0f;
+      const int g = col / q_len;
+      const int i = col - g * q_len;
+      const int64_t h = (int64_t)kvh * p.group + g;
+      if (direct) {
+        const int64_t row = (int64_t)b * q_len + i;
+        QT *dst = reinterpret_cast<QT *>(p.out) + row * p.o_srow + h * p.o_shead + DPL * j;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          if constexpr (D == 128) {
+            i32x4 w;
+#pragma unroll
+            for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<QT>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+            *reinterpret_cast<i32x4 *>(dst + rr * NT) = w;
+          } else {
+            i32x2 w;
+#pragma unroll
+            for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<QT>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+            *reinterpret_cast<i32x2 *>(dst + rr * NT) = w;
+          }
+        }
+        if (j == 0 && p.lse) {
+          const float m = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
+          // v_log_f32 is log2
+          p.lse[row * p.lse_srow + h * p.lse_shead] = (l_tot > 0.0f) ? kLn2 * (m + __builtin_amdgcn_logf(l_tot)) : -INFINITY;
+        }
+        if (j == 0 && mark_final) p.pm[row * p.pm_srow + h * p.pm_shead] = INFINITY;  // merge: already final
+      } else {
+        const int64_t prow = slot_row * q_len + i;
+        const int64_t po_idx = prow * p.po_srow + h * p.po_shead + slot_split * p.po_ssplit + DPL * j;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          if (p.po_f32) {
+            float *dst = reinterpret_cast<float *>(p.po) + po_idx + rr * NT;
+#pragma unroll
+            for (int t = 0; t < NT; t += 4)
+              *reinterpret_cast<f32x4 *>(dst + t) = f32x4{acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv,
+                                                          acc[qt][t + 2][rr] * inv, acc[qt][t + 3][rr] * inv};
+          } else {
+            _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx + rr * NT;
+            if constexpr (D == 128) {
+              i32x4 w;
+#pragma unroll
+              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+              *reinterpret_cast<i32x4 *>(dst) = w;
+            } else {
+              i32x2 w;
+#pragma unroll
+              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+              *reinterpret_cast<i32x2 *>(dst) = w;
+            }
+          }
+        }
+        if (j == 0) {
+          p.pm[prow * p.pm_srow + h * p.pm_shead + slot_split * p.pm_ssplit] = m_run[qt];
+          p.pl[prow * p.pl_srow + h * p.pl_shead + slot_split * p.pl_ssplit] = l_tot;
+        }
+      }
+    }
+  }
+};
+
 // Splits of sequence b taken by the static first round: workgroup w starts
 // on slot w of the split-major numbering (sequence w % B, split w / B).
 __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G ? (G - 1 - b) / B + 1 : 0; }
@@ -310,21 +711,12 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // fp32 partial (o / l, m, l) at its split slot.
 template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
-  typedef typename MfmaTypes<QT>::vec8 qvec8;
-  typedef typename KvBlock<KT, D>::type Block;
-  // Softmax probabilities: f16 for fp8 caches (V converted to f16), the
-  // cache's own type for 16-bit caches.
-  typedef typename std::conditional<KT == 0, _Float16, QT>::type PT;
-  typedef typename MfmaTypes<PT>::vec8 pvec8;
-  constexpr int kTok = KT == 0 ? 32 : 16;  // tokens per block
-  // bf16 probabilities carry 8 significant bits: split P = hi + lo (both
-  // bf16) and accumulate both products, which restores ~16 bits.
-  constexpr bool kSplitP = KT == 1 && std::is_same<QT, __bf16>::value;
+  typedef KvUnit<QT, KT, D, NQT, TREE> U;
+  typedef typename U::qvec8 qvec8;
+  typedef typename U::Block Block;
+  constexpr int kTok = U::kTok;            // tokens per block
   constexpr int kLeadMul = 32 / kTok;      // hand-off leads in 32-token units
-  constexpr int NCH = D / 64;  // 64-byte K chunks per token row
-  constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
-  constexpr int NT = D / 16;   // 16-row d tiles of the PV product
-  constexpr int DPL = D / 4;   // contiguous output dims per lane
+  constexpr int NS = U::NS;
   // One query tile: the next unit's query operand is prefetched into a second
   // register set.  Two tiles: it is loaded once the current unit's last block
   // has been computed.
@@ -346,7 +738,6 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   const int n16 = lane & 15;
   const int j = lane >> 4;
   const int q_len = p.q_len;
-  const int mcols = p.group * q_len;
   const int B = p.batch;
   const int S = p.split_size;
   const int G = gridDim.x;
@@ -392,102 +783,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     }
     return v;
   };
-  // Query operand (B of S^T = K . Q^T): column n' = 16*qt + lane%16.
-  // Tree verification: ancestor words of this lane's query columns over the
-  // newest q_len keys (bit j lets the column see key L - q_len + j).  The
-  // causal rule (TREE = false) keeps no words: its limit is recomputed per
-  // unit, which keeps the tree state out of the causal kernels' registers.
-  auto load_tree = [&](int b, int (&dst)[TREE ? NQT : 1]) {
-    if constexpr (TREE) {
-#pragma unroll
-      for (int qt = 0; qt < NQT; ++qt) {
-        const int col = 16 * qt + n16;
-        dst[qt] = col < mcols ? p.tree[(int64_t)b * p.tree_sb + (col % q_len)] : 0;
-      }
-    }
-  };
-  auto load_q = [&](int b, int kvh, qvec8 (&dst)[NQT][NS]) {
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-      const int col = 16 * qt + n16;
-      const int g = col / q_len;
-      const int i = col - g * q_len;
-      if (col < mcols) {
-        const QT *qrow = reinterpret_cast<const QT *>(p.q) + (int64_t)(b * q_len + i) * p.q_srow +
-                         (int64_t)(kvh * p.group + g) * p.q_shead;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const int d0 = (s >> 1) * 64 + 16 * j + (s & 1) * 8;
-          dst[qt][s] = __builtin_bit_cast(qvec8, *reinterpret_cast<const i32x4 *>(qrow + d0));
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) dst[qt][s] = __builtin_bit_cast(qvec8, i32x4{0, 0, 0, 0});
-      }
-    }
-  };
-  // Raw buffer loads through a per-page resource: the page base lives in
-  // SGPRs, one 32-bit lane offset serves every K (V) load of the page and the
-  // hardware range check (the page's byte extent) returns zeros for anything
-  // outside it.  Loads are unconditional -- an invalid page id reads page 0 --
-  // and compute_block zeroes V of every token outside the split or on an
-  // invalid page.  Lane offsets inside a page fit in 32 bits (checked on the
-  // host).
+  auto load_tree = [&](int b, int (&dst)[TREE ? NQT : 1]) { U::load_tree(p, b, dst, n16); };
+  auto load_q = [&](int b, int kvh, qvec8 (&dst)[NQT][NS]) { U::load_q(p, b, kvh, dst, n16, j); };
   // parts: 1 = the K loads, 2 = the V loads, 3 = both (a constant at every call)
   auto load_block = [&](Block &r, int pid, int kvh, int blk, int parts = 3) {
-    if constexpr (KT == 1) {
-      // 16-bit elements: one page per block; K slice s at byte 128*(s/2) + 16*(s%2)
-      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 32 * j);
-      const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + 2 * (D / 16) * n16);
-      const int raw_page = __builtin_amdgcn_readlane(pid, blk);
-      const int page = raw_page >= 0 ? raw_page : 0;
-      if (parts & 1) {
-        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-          r.k[s] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 128 * (s >> 1) + 16 * (s & 1), kStreamPolicy));
-      }
-      if (parts & 2) {
-        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (D == 128)
-            r.v[e] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, e * p.v_stok32, kStreamPolicy));
-          else
-            r.v[e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
-        }
-      }
-      return;
-    }
-    else {
-    const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
-    const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
-#pragma unroll
-    for (int T = 0; T < 2; ++T) {
-      const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
-      const int page = raw_page >= 0 ? raw_page : 0;
-      if (parts & 1) {
-        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, kStreamPolicy));
-      }
-      if (parts & 2) {
-        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (D == 128)
-            r.v[4 * T + e] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, voff, e * p.v_stok32, kStreamPolicy));
-          else
-            r.v[4 * T + e] = (int)__builtin_amdgcn_raw_buffer_load_b32(vr, voff, e * p.v_stok32, kStreamPolicy);
-        }
-      }
-    }
-    }
+    U::load_block(p, r, pid, kvh, blk, parts, n16, j);
   };
 
   // ---- stream state (wave-uniform except the VGPR operands) ----
@@ -791,187 +1091,11 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // the last key that every column sees
       const int min_lim = min(uEnd - 1, TREE ? draft0 - 1 : draft0);
 
-      f32x4 acc[NQT][NT];
-      float m_run[NQT], l_run[NQT];
-#pragma unroll
-      for (int qt = 0; qt < NQT; ++qt) {
-        m_run[qt] = -INFINITY;
-        l_run[qt] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-
+      U st;
+      st.reset();
       auto compute_block = [&](Block &r, int blk, auto &&after_scores) {
-        const int tok0 = uStart + kTok * blk;
-        // Tokens past the split (the tail of the sequence's last page, or a
-        // tile beyond the split read from page 0) and tokens of an invalid
-        // page may hold arbitrary bytes, NaN codes included: zero their V so
-        // that p = 0 contributes exactly 0.  K needs no fix-up: their scores
-        // are replaced by -inf below.  A 16-bit block has one tile; its
-        // second-tile slots are empty (score -inf, V zero).
-        const bool bad0 = __builtin_amdgcn_readlane(pidU, KT == 0 ? 2 * blk : blk) < 0;
-        const bool bad1 = KT == 0 ? __builtin_amdgcn_readlane(pidU, 2 * blk + 1) < 0 : true;
-        if constexpr (KT == 0) {
-          if (tok0 + 32 > uEnd || bad0 || bad1) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-              if (t >= uEnd || ((e >> 2) ? bad1 : bad0)) {
-                if constexpr (D == 128)
-                  r.v[e] = i32x2{0, 0};
-                else
-                  r.v[e] = 0;
-              }
-            }
-          }
-        } else {
-          if (tok0 + 16 > uEnd || bad0) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if (tok0 + 4 * j + e >= uEnd || bad0) {
-                if constexpr (D == 128)
-                  r.v[e] = i32x4{0, 0, 0, 0};
-                else
-                  r.v[e] = i32x2{0, 0};
-              }
-            }
-          }
-        }
-        // ---- S^T = K . Q^T ----
-        f32x4 sc[NQT][2];
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-          sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-          sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        if constexpr (KT == 0) {
-#pragma unroll
-          for (int T = 0; T < 2; ++T) {
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-              const i32x4 raw = r.k[T][s >> 1];
-              const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
-#pragma unroll
-              for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const qvec8 kop = __builtin_bit_cast(qvec8, r.k[s]);
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) sc[qt][0] = mfma16(kop, qop[qt][s], sc[qt][0]);
-          }
-        }
-        // r.k is consumed: the refill's K loads may overwrite it
-        after_scores();
-        // ---- online softmax (log2 domain) ----
-        const bool need_mask = (tok0 + kTok - 1 > min_lim) || bad0 || bad1;
-        pvec8 pop[NQT];
-        pvec8 pop_lo[kSplitP ? NQT : 1];
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-          float x[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = sc[qt][e >> 2][e & 3] * c_log2;
-          if (need_mask) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int t = tok0 + 16 * (e >> 2) + 4 * j + (e & 3);
-              bool vis;
-              if constexpr (TREE)
-                vis = t < uEnd && (t < draft0 || (((uint32_t)treeU[qt] >> ((t - draft0) & 31)) & 1u));
-              else
-                vis = t <= lim[qt];
-              x[e] = (vis && !((e >> 2) ? bad1 : bad0)) ? x[e] : -INFINITY;
-            }
-          }
-          float mloc = x[0];
-#pragma unroll
-          for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, x[e]);
-          mloc = wave_max_xor16_32(mloc);
-          // Lazy rescale: the reference max m_run only moves when some
-          // column's block max exceeds it by more than kRescaleLog2 (or it is
-          // still -inf).  P and l always use the same m_run, so the result is
-          // exact up to rounding; p stays below 2^kRescaleLog2 (f16 range).
-          if (__any(mloc > m_run[qt] + kRescaleLog2)) {
-            const float m_new = fmaxf(m_run[qt], mloc);
-            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_use);
-            l_run[qt] *= alpha;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[qt][t] *= alpha;
-            m_run[qt] = m_new;
-          }
-          const float m_use = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
-          float psum = 0.0f;
-          i32x4 pw, pw_lo;
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(x[e] - m_use);
-            const float p1 = __builtin_amdgcn_exp2f(x[e + 1] - m_use);
-            psum += p0 + p1;
-            pw[e >> 1] = pack2<PT>(p0, p1);
-            if constexpr (kSplitP) {
-              // bf16 -> f32 is exact: the halves are the top 16 bits of an f32
-              const uint32_t w = (uint32_t)pw[e >> 1];
-              pw_lo[e >> 1] = pack2<PT>(p0 - __builtin_bit_cast(float, w << 16),
-                                        p1 - __builtin_bit_cast(float, w & 0xffff0000u));
-            }
-          }
-          pop[qt] = __builtin_bit_cast(pvec8, pw);
-          if constexpr (kSplitP) pop_lo[qt] = __builtin_bit_cast(pvec8, pw_lo);
-          l_run[qt] += psum;
-        }
-        // ---- O^T += V^T . P^T ----
-        // d tile t (0 <= t < D/16) holds dims 8*(lane%16) + t (D = 128) or
-        // 4*(lane%16) + t (D = 64); k slot i of the V^T and P^T operands is
-        // token 16*(i/4) + 4*(lane/16) + i%4 of the block.
-#pragma unroll
-        for (int tp2 = 0; tp2 < NT; tp2 += 2) {
-          i32x4 wa, wb;
-          if constexpr (KT == 0) {
-            // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-              int w0, w1;
-              if constexpr (D == 128) {
-                w0 = r.v[e][tp2 >> 2];
-                w1 = r.v[e + 1][tp2 >> 2];
-              } else {
-                w0 = r.v[e];
-                w1 = r.v[e + 1];
-              }
-              const f32x2 f0 = fp8x2_f32(w0, (tp2 & 3) != 0);
-              const f32x2 f1 = fp8x2_f32(w1, (tp2 & 3) != 0);
-              wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
-              wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
-            }
-          } else {
-            // d tiles tp2, tp2+1 are the low and high halves of dword tp2 / 2:
-            // pair the halves of tokens (0, 1) and (2, 3); slots 4-7 are empty
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-              const uint32_t w0 = (uint32_t)r.v[e][tp2 >> 1];
-              const uint32_t w1 = (uint32_t)r.v[e + 1][tp2 >> 1];
-              wa[e >> 1] = (int)((w0 & 0xffffu) | (w1 << 16));
-              wb[e >> 1] = (int)((w0 >> 16) | (w1 & 0xffff0000u));
-            }
-            wa[2] = wa[3] = 0;
-            wb[2] = wb[3] = 0;
-          }
-          const pvec8 va = __builtin_bit_cast(pvec8, wa);
-          const pvec8 vb = __builtin_bit_cast(pvec8, wb);
-#pragma unroll
-          for (int qt = 0; qt < NQT; ++qt) {
-            acc[qt][tp2] = mfma16(va, pop[qt], acc[qt][tp2]);
-            acc[qt][tp2 + 1] = mfma16(vb, pop[qt], acc[qt][tp2 + 1]);
-            if constexpr (kSplitP) {
-              acc[qt][tp2] = mfma16(va, pop_lo[qt], acc[qt][tp2]);
-              acc[qt][tp2 + 1] = mfma16(vb, pop_lo[qt], acc[qt][tp2 + 1]);
-            }
-          }
-        }
+        st.compute_block(r, pidU, blk, uStart + kTok * blk, uEnd, draft0, lim, min_lim, treeU, qop, c_log2, j,
+                         after_scores);
       };
 
       // Compute block k, then refill its buffer with stream position k + 2:
@@ -1029,74 +1153,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           load_tree(nB, treeU);
         }
 
-      // ---- epilogue: this lane holds column 16*qt + lane%16, dims [DPL*j, DPL*j + DPL) ----
-#pragma unroll
-      for (int qt = 0; qt < NQT; ++qt) {
-        const float l_tot = wave_sum_xor16_32(l_run[qt]);
-        const int col = 16 * qt + n16;
-        if (col >= mcols) continue;
-        const float inv = (l_tot > 0.0f) ? v_scale / l_tot : 0.0f;
-        const int g = col / q_len;
-        const int i = col - g * q_len;
-        const int64_t row = (int64_t)b * q_len + i;
-        const int64_t h = (int64_t)kvh * p.group + g;
-        if (direct) {
-          QT *dst = reinterpret_cast<QT *>(p.out) + row * p.o_srow + h * p.o_shead + DPL * j;
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            if constexpr (D == 128) {
-              i32x4 w;
-#pragma unroll
-              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<QT>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
-              *reinterpret_cast<i32x4 *>(dst + rr * NT) = w;
-            } else {
-              i32x2 w;
-#pragma unroll
-              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<QT>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
-              *reinterpret_cast<i32x2 *>(dst + rr * NT) = w;
-            }
-          }
-          if (j == 0 && p.lse) {
-            const float m = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
-            // v_log_f32 is log2
-            p.lse[row * p.lse_srow + h * p.lse_shead] =
-                (l_tot > 0.0f) ? kLn2 * (m + __builtin_amdgcn_logf(l_tot)) : -INFINITY;
-          }
-          if (j == 0 && has_ws) p.pm[row * p.pm_srow + h * p.pm_shead] = INFINITY;  // merge: already final
-        } else {
-          const int64_t po_idx = row * p.po_srow + h * p.po_shead + (int64_t)split * p.po_ssplit + DPL * j;
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            if (p.po_f32) {
-              float *dst = reinterpret_cast<float *>(p.po) + po_idx + rr * NT;
-#pragma unroll
-              for (int t = 0; t < NT; t += 4)
-                *reinterpret_cast<f32x4 *>(dst + t) = f32x4{acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv,
-                                                            acc[qt][t + 2][rr] * inv, acc[qt][t + 3][rr] * inv};
-            } else {
-              _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx + rr * NT;
-              if constexpr (D == 128) {
-                i32x4 w;
-#pragma unroll
-                for (int t = 0; t < NT; t += 2)
-                  w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
-                *reinterpret_cast<i32x4 *>(dst) = w;
-              } else {
-                i32x2 w;
-#pragma unroll
-                for (int t = 0; t < NT; t += 2)
-                  w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
-                *reinterpret_cast<i32x2 *>(dst) = w;
-              }
-            }
-          }
-          if (j == 0) {
-            float *pm = p.pm + row * p.pm_srow + h * p.pm_shead;
-            pm[(int64_t)split * p.pm_ssplit] = m_run[qt];
-            p.pl[row * p.pl_srow + h * p.pl_shead + (int64_t)split * p.pl_ssplit] = l_tot;
-          }
-        }
-      }
+      // ---- epilogue ----
+      st.finish(p, b, kvh, direct, b, split, direct && has_ws, v_scale, n16, j);
 
       // ---- the next unit inherits the stream ----
       par = (par + nU) % NB;
@@ -1534,8 +1592,7 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE, NB>, threads,
-                                                     lds) !=
-            hipSuccess ||
+                                                     lds) != hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
     cached_dev = dev;
@@ -1699,12 +1756,57 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.indptr = a.page_indptr;
   pp.tree = a.tree_mask;
   pp.tree_sb = a.tree_mask_stride_batch;
-  // consecutive launches take consecutive queue slots (launches that overlap
-  // on one device, from different streams, never share counters)
-  static std::atomic<unsigned int> launch_seq{0};
-  pp.queue_slot = (int)(launch_seq.fetch_add(1u, std::memory_order_relaxed) % l20pd::kQueueSlots);
   return pp;
 }
+
+// Work-queue counter slots of the split schedule, per device.  Launches on one stream run in order and share the
+// stream's slot; a launch captured into a graph takes the next slot of a
+// separate pool, since the graph may replay on any stream.  More streams in
+// use at once than eager slots share slots (least recently used first).
+constexpr int kCaptureSlots = 16;
+struct SlotEntry {
+  int dev;
+  void *stream;
+  int slot;
+  uint64_t used;
+};
+std::mutex g_slot_mu;
+std::vector<SlotEntry> g_slots;
+uint64_t g_slot_clock = 0;
+std::atomic<unsigned int> g_capture_seq{0};
+
+int counter_slot(hipStream_t stream) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusActive)
+    return l20pd::kQueueSlots - kCaptureSlots + (int)(g_capture_seq.fetch_add(1u) % kCaptureSlots);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(g_slot_mu);
+  const uint64_t now = ++g_slot_clock;
+  for (SlotEntry &e : g_slots)
+    if (e.dev == dev && e.stream == (void *)stream) {
+      e.used = now;
+      return e.slot;
+    }
+  constexpr int kEager = l20pd::kQueueSlots - kCaptureSlots;
+  bool taken[kEager] = {};
+  SlotEntry *lru = nullptr;
+  for (SlotEntry &e : g_slots)
+    if (e.dev == dev) {
+      taken[e.slot] = true;
+      if (!lru || e.used < lru->used) lru = &e;
+    }
+  for (int sl = 0; sl < kEager; ++sl)
+    if (!taken[sl]) {
+      g_slots.push_back(SlotEntry{dev, (void *)stream, sl, now});
+      return sl;
+    }
+  lru->stream = (void *)stream;
+  lru->used = now;
+  return lru->slot;
+}
+
+
 
 l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
   l20pd::MergeParams mp;
@@ -1757,7 +1859,8 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   const int group = a->num_q_heads / a->num_kv_heads;
   const int nqt = (group * a->q_len + 15) / 16;
-  const l20pd::PartialParams pp = partial_params(*a, n_s);
+  l20pd::PartialParams pp = partial_params(*a, n_s);
+  pp.queue_slot = counter_slot(stream);
   const l20pd::MergeParams mp = merge_params(*a, pp.num_splits);
   const bool bf16 = a->query_dtype == L20_PD_BF16;
   const int rows = a->batch * a->q_len;

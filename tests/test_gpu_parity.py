@@ -378,8 +378,8 @@ def test_hip_graph_capture_replays_match_eager(max_wg, monkeypatch):
 
 
 def test_queue_counters_reset_across_slot_reuse(monkeypatch):
-    """150 back-to-back queue-driven launches wrap the 64 work-queue slots
-    twice; each launch must start on a counter its slot's previous launch
+    """150 back-to-back queue-driven launches on one stream share the stream's
+    work-queue slot; each launch must start on a counter the previous launch
     reset (a stale counter would skip items and change the result)."""
     import l20_pd_cabi as cabi
 
