@@ -288,9 +288,13 @@ struct KvUnit {
   typedef typename std::conditional<KT == 0, _Float16, QT>::type PT;
   typedef typename MfmaTypes<PT>::vec8 pvec8;
   static constexpr int kTok = KT == 0 ? 32 : 16;  // tokens per block
-  // bf16 probabilities carry 8 significant bits: split P = hi + lo (both
-  // bf16) and accumulate both products, which restores ~16 bits.
-  static constexpr bool kSplitP = KT == 1 && std::is_same<QT, __bf16>::value;
+  // P is rounded to the MFMA operand type, 11 significant bits (f16) or 8
+  // (bf16), while the softmax denominator sums it unrounded.  Equal scores
+  // round alike, so the error does not average out: with every other key at
+  // p = 2^-0.1 and V = +-448 it reaches ~0.1 absolute.  Split P = hi + lo
+  // (hi = rnd(p), lo = rnd(p - hi)) and accumulate both products: ~22 (f16) or
+  // ~16 (bf16) bits.
+  static constexpr bool kSplitP = true;
   static constexpr int NCH = D / 64;  // 64-byte K chunks per token row
   static constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
   static constexpr int NT = D / 16;   // 16-row d tiles of the PV product
@@ -535,9 +539,17 @@ struct KvUnit {
         psum += p0 + p1;
         pw[e >> 1] = pack2<PT>(p0, p1);
         if constexpr (kSplitP) {
-          // bf16 -> f32 is exact: the halves are the top 16 bits of an f32
-          const uint32_t w = (uint32_t)pw[e >> 1];
-          pw_lo[e >> 1] = pack2<PT>(p0 - __builtin_bit_cast(float, w << 16), p1 - __builtin_bit_cast(float, w & 0xffff0000u));
+          if constexpr (std::is_same<PT, __bf16>::value) {
+            // bf16 -> f32 is exact: the halves are the top 16 bits of an f32
+            const uint32_t w = (uint32_t)pw[e >> 1];
+            pw_lo[e >> 1] =
+                pack2<PT>(p0 - __builtin_bit_cast(float, w << 16), p1 - __builtin_bit_cast(float, w & 0xffff0000u));
+          } else {
+            // f16 round trips of p0 and p1 themselves (the same RNE rounding as
+            // the packed word): ROCm 7.2's LLVM folds element extraction from
+            // the packed words of this loop into the first pair's halves.
+            pw_lo[e >> 1] = pack2<PT>(p0 - (float)(_Float16)p0, p1 - (float)(_Float16)p1);
+          }
         }
       }
       pop[qt] = __builtin_bit_cast(pvec8, pw);

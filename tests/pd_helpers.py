@@ -5,8 +5,8 @@ oracle on the same bytes, and compare to the stated tolerances.
 Tolerances (bf16/fp16 output vs the fp32 dequantise-then-attend oracle):
 max |diff| <= 1e-2 and per-(row, head) cosine >= 0.9999; natural-log LSE
 |diff| <= 1e-4 * max(1, |lse|).  FP8 -> fp32 dequantisation is exact, so only
-accumulation order (and the f16 rounding of softmax probabilities on the MFMA
-path) separates the two.
+accumulation order (and the ~22-bit hi + lo split of the softmax probabilities
+on the MFMA path) separates the two.
 """
 
 from __future__ import annotations
