@@ -153,9 +153,34 @@ int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args);
 /* Enqueue the split-KV partial kernel and the LSE merge kernel on `stream`
  * (hipStream_t, NULL = default stream).  Asynchronous; allocates nothing.
  * Requires kv_dtype == L20_PD_KV_FP8_E4M3.  Calls on different streams of one
- * device may overlap (each with its own workspace and output): consecutive
- * calls use different work-queue counters, 64 of them per device. */
+ * device may overlap (each with its own workspace and output): the partial
+ * kernel's work-queue counters (64 slots per device) are given per stream --
+ * calls on one stream run in order and share its slot, up to 48 streams get
+ * slots of their own (least recently used ones are shared beyond that), and a
+ * call captured into a HIP graph takes one of 16 further slots in turn, since
+ * the graph may replay on any stream.
+ * (<- l20_paged_decode_fp8_e4m3_split_out_cuda, l20_paged_decode.cu:651-725) */
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
+
+/* Device-side errors of the partial kernel (no counterpart in the reference,
+ * whose kernels have no inter-wave waits).  Its hand-off waits between the
+ * waves of a workgroup give up after ~0.1 s of polling instead of hanging;
+ * the wave records one of these codes and exits normally (its results are
+ * then incomplete).  Returns the bitwise OR of the codes recorded on the
+ * current device since the last clear (0: none), or -L20_PD_ELAUNCH on a HIP
+ * error.  Synchronizes the device.  clear != 0 zeroes the error words and
+ * the work-queue counters of the slots that had one; call it only while no
+ * call of this library is in flight. */
+#define L20_PD_DEVERR_PREFIX_WAIT 1   /* the per-sequence item table was never published */
+#define L20_PD_DEVERR_ACK_WAIT 2      /* a wave never acknowledged the published item */
+#define L20_PD_DEVERR_PUBLISH_WAIT 4  /* the next item was never published */
+int32_t l20_pd_device_errors(int32_t clear);
+
+/* Polls before a hand-off wait gives up, on the current device (0 restores
+ * the default, ~0.1 s of polling).  A test hook with no reference
+ * counterpart: a limit of 1 makes the waits give up at once, which exercises
+ * the give-up path while every kernel still exits normally.  Synchronous. */
+int32_t l20_pd_set_spin_limit(uint32_t polls);
 
 /* Allocation-free variant of l20_pd_fp8_e4m3_split_out (no counterpart in the
  * reference: for callers that cannot allocate device memory, such as code

@@ -270,6 +270,17 @@ __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 
 // (different streams).
 constexpr int kQueueSlots = 64;
 __device__ __align__(64) unsigned int g_pd_queue[kQueueSlots][16];
+// Hand-off waits give up after this many polls (s_sleep 1 each, ~0.1 s in
+// all; a wait that the protocol satisfies ends within microseconds).  A wave
+// that gives up ORs an L20_PD_DEVERR_* code into g_pd_error[slot], takes no
+// further item and exits normally, so a hand-off bug shows up as an error
+// (l20_pd_device_errors) instead of a hung GPU.
+constexpr unsigned int kSpinLimit = 1u << 22;
+__device__ unsigned int g_pd_error[kQueueSlots];
+// Polls before a wait gives up: kSpinLimit unless lowered through
+// l20_pd_set_spin_limit (tests force the give-up path with it).  Read when a
+// wait starts, so the block stream holds no register for it.
+__device__ unsigned int g_pd_spin_limit = kSpinLimit;
 
 // ---------------------------------------------------------------------------
 // Per-unit math of the partial kernel
@@ -951,13 +962,31 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   auto claim_point = [&]() {
     if (wave == 0 && more && !claimed) issue_claim();
   };
+  // Bounded polling: a wait loop counts its polls and stops at the limit;
+  // past the loop, a wait that gave up records its error code.
+  auto spin_cap = []() { return __builtin_amdgcn_readfirstlane(uniform_ld(&g_pd_spin_limit, 0)); };
+  auto record_give_up = [&](unsigned int code) {
+    if (lane == 0) __hip_atomic_fetch_or(&g_pd_error[p.queue_slot], code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   // Wave 0: the next item into (db, ds, dL); db = -1 when none is left.
   auto resolve = [&]() {
     db = -1;
     if (!more) return;
     if (!claimed) issue_claim();
-    if (compact)
-      while (!__builtin_amdgcn_readfirstlane(lds_poll(&s_prefix_ready))) __builtin_amdgcn_s_sleep(1);
+    if (compact) {
+      unsigned int polls = 0;
+      if (!__builtin_amdgcn_readfirstlane(lds_poll(&s_prefix_ready))) {
+        const unsigned int cap = spin_cap();
+        while (!__builtin_amdgcn_readfirstlane(lds_poll(&s_prefix_ready)) && ++polls < cap)
+          __builtin_amdgcn_s_sleep(1);
+        if (polls < cap) polls = 0;
+      }
+      if (__builtin_expect(polls != 0, 0)) {
+        record_give_up(L20_PD_DEVERR_PREFIX_WAIT);
+        more = false;
+        return;
+      }
+    }
     const int64_t Q = queue_total();
     for (;;) {
       const int64_t c = __builtin_amdgcn_readfirstlane(claim);
@@ -983,8 +1012,16 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     const int slot = t_item & 1;
     if (wave == 0) {
       resolve();
-      while (__builtin_amdgcn_readfirstlane(lds_poll(&s_ack[slot])) < nwaves - 1)
-        __builtin_amdgcn_s_sleep(1);
+      unsigned int polls = 0;
+      if (__builtin_amdgcn_readfirstlane(lds_poll(&s_ack[slot])) < nwaves - 1) {
+        const unsigned int cap = spin_cap();
+        while (__builtin_amdgcn_readfirstlane(lds_poll(&s_ack[slot])) < nwaves - 1 && ++polls < cap)
+          __builtin_amdgcn_s_sleep(1);
+        if (polls < cap) polls = 0;
+      }
+      // A wave that never acknowledged the slot's previous item may read the
+      // new one instead (valid indices, wrong results, the error recorded).
+      if (__builtin_expect(polls != 0, 0)) record_give_up(L20_PD_DEVERR_ACK_WAIT);
       if (lane == 0) {
         lds_put(&s_ack[slot], 0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the reset ahead of the publication
@@ -998,9 +1035,17 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       nL = dL;
       return true;
     }
-    while (__builtin_amdgcn_readfirstlane(lds_poll(&s_seq[slot])) != t_item) {
+    if (__builtin_amdgcn_readfirstlane(lds_poll(&s_seq[slot])) != t_item) {
       if (!wait) return false;
-      __builtin_amdgcn_s_sleep(1);
+      const unsigned int cap = spin_cap();
+      unsigned int polls = 0;
+      while (__builtin_amdgcn_readfirstlane(lds_poll(&s_seq[slot])) != t_item && ++polls < cap)
+        __builtin_amdgcn_s_sleep(1);
+      if (__builtin_expect(polls >= cap, 0)) {
+        record_give_up(L20_PD_DEVERR_PUBLISH_WAIT);
+        nb = -1;  // this wave stops after its current unit
+        return true;
+      }
     }
     nb = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][0]));
     ns = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][1]));
@@ -1768,6 +1813,7 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.indptr = a.page_indptr;
   pp.tree = a.tree_mask;
   pp.tree_sb = a.tree_mask_stride_batch;
+
   return pp;
 }
 
@@ -1990,6 +2036,46 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
 }
 
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { return run(a, stream, kBoth, kKvFp8); }
+
+int32_t l20_pd_set_spin_limit(uint32_t polls) {
+  g_last_error[0] = '\0';
+  const unsigned int v = polls ? polls : l20pd::kSpinLimit;
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_spin_limit), &v, sizeof(v), 0, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "l20_pd_set_spin_limit: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
+int32_t l20_pd_device_errors(int32_t clear) {
+  g_last_error[0] = '\0';
+  unsigned int err[l20pd::kQueueSlots];
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(err, HIP_SYMBOL(l20pd::g_pd_error), sizeof(err), 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "l20_pd_device_errors: %s", hipGetErrorString(e));
+    return -L20_PD_ELAUNCH;
+  }
+  unsigned int all = 0;
+  for (int sl = 0; sl < l20pd::kQueueSlots; ++sl) {
+    all |= err[sl];
+    if (clear && err[sl]) {
+      // a launch that gave up may have left its work-queue counter mid-way
+      const unsigned int zero[16] = {0};
+      const unsigned int none = 0;
+      e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_queue), zero, sizeof(zero), sizeof(zero) * sl, hipMemcpyHostToDevice);
+      if (e == hipSuccess)
+        e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_error), &none, sizeof(none), sizeof(none) * sl,
+                              hipMemcpyHostToDevice);
+      if (e != hipSuccess) {
+        snprintf(g_last_error, sizeof(g_last_error), "l20_pd_device_errors: %s", hipGetErrorString(e));
+        return -L20_PD_ELAUNCH;
+      }
+    }
+  }
+  return (int32_t)all;
+}
 
 int32_t l20_pd_fp8_e4m3_split_out_noalloc(const l20_pd_fp8_args *a, void *stream) {
   g_last_error[0] = '\0';

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).with_name("libl20_paged_decode_hip.so")
 L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
 L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
 L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16 = 0, 1, 2
+L20_PD_DEVERR_PREFIX_WAIT, L20_PD_DEVERR_ACK_WAIT, L20_PD_DEVERR_PUBLISH_WAIT = 1, 2, 4
 ABI_VERSION = 3
 
 # Every extern "C" symbol declared in include/*.h.
@@ -27,6 +28,8 @@ EXPORTED = (
     "l20_pd_fp8_e4m3_check",
     "l20_pd_fp8_e4m3_split_out",
     "l20_pd_fp8_e4m3_split_out_noalloc",
+    "l20_pd_device_errors",
+    "l20_pd_set_spin_limit",
     "l20_pd_split_out",
     "l20_pd_fp8_e4m3_partial",
     "l20_pd_fp8_e4m3_merge",
@@ -110,6 +113,10 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
                  "l20_pd_fp8_e4m3_partial", "l20_pd_fp8_e4m3_merge"):
         getattr(lib, name).argtypes = [args_p, _vp]
         getattr(lib, name).restype = _i32
+    lib.l20_pd_device_errors.argtypes = [_i32]
+    lib.l20_pd_device_errors.restype = _i32
+    lib.l20_pd_set_spin_limit.argtypes = [ctypes.c_uint32]
+    lib.l20_pd_set_spin_limit.restype = _i32
     lib.l20_pd_default_split_size.argtypes = [_i32, _i32, _i32, _i32]
     lib.l20_pd_default_split_size.restype = _i32
     lib.l20_pd_fp8_e4m3_dequant_f32.argtypes = [_vp, _vp, _i64, _f32, _vp]
@@ -242,6 +249,23 @@ def partial(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = No
 def merge(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
     """Enqueue only the LSE merge kernel."""
     _call("l20_pd_fp8_e4m3_merge", args, stream, lib)
+
+
+def device_errors(clear: bool = False, lib: Optional[ctypes.CDLL] = None) -> int:
+    """``l20_pd_device_errors``: OR of the L20_PD_DEVERR_* codes the partial
+    kernel recorded on the current device (synchronizes it)."""
+    lib = lib or load()
+    rc = lib.l20_pd_device_errors(1 if clear else 0)
+    if rc < 0:
+        raise RuntimeError(last_error(lib))
+    return rc
+
+
+def set_spin_limit(polls: int, lib: Optional[ctypes.CDLL] = None) -> None:
+    """``l20_pd_set_spin_limit`` (0 restores the default)."""
+    lib = lib or load()
+    if lib.l20_pd_set_spin_limit(int(polls)) != L20_PD_OK:
+        raise RuntimeError(last_error(lib))
 
 
 def check(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> None:
