@@ -51,7 +51,10 @@ enum l20_pd_dtype {
 enum l20_pd_kv_dtype {
   L20_PD_KV_FP8_E4M3 = 0,  /* OCP e4m3fn codes, dequantised as code * scale */
   L20_PD_KV_FP16 = 1,      /* fp16 values (query must be fp16) */
-  L20_PD_KV_BF16 = 2       /* bf16 values (query must be bf16) */
+  L20_PD_KV_BF16 = 2,      /* bf16 values (query must be bf16) */
+  L20_PD_KV_FP8_E5M2 = 3   /* OCP e5m2 codes, dequantised as code * scale (the fp8 entry
+                              points; the reference's hook-facing Triton path accepts
+                              torch.float8_e5m2 caches, integrations/vllm/l20_paged_split_kv.py:617-621) */
 };
 
 /* Return codes. */

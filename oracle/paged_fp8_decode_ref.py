@@ -1,4 +1,4 @@
-"""CPU oracle for paged FP8 (OCP e4m3fn) KV-cache decode attention.
+"""CPU oracle for paged FP8 (OCP e4m3fn, or e5m2) KV-cache decode attention.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
@@ -30,6 +30,9 @@ How each function is pinned (tests/test_oracle.py):
 * ``e4m3fn_decode_table``: all 256 codes against the closed form
   ``(-1)^s 2^(e-7) (1 + m/8)`` / ``2^-6 m/8`` and against torch's own
   ``float8_e4m3fn -> float32`` conversion.
+* ``e5m2_decode_table``: all 256 codes against torch's ``float8_e5m2 ->
+  float32`` conversion and against the top byte of an fp16 (e5m2 is fp16
+  with the low 8 mantissa bits dropped: code ``c`` is the fp16 ``c << 8``).
 * ``encode_e4m3fn`` / ``quantize_*``: against torch's ``.to(float8_e4m3fn)``
   (round-to-nearest-even) on random values and on every midpoint between
   adjacent codes.
@@ -95,6 +98,47 @@ _POSITIVE = _DECODE[:0x7F].astype(np.float64)
 def e4m3fn_to_f32(codes: np.ndarray) -> np.ndarray:
     """Decode uint8 e4m3fn codes to float32 (exact)."""
     return _DECODE[np.asarray(codes, dtype=np.uint8)]
+
+
+def e5m2_decode_table() -> np.ndarray:
+    """float32 value of each of the 256 OCP e5m2 codes.
+
+    Bit layout s.eeeee.mm, exponent bias 15, IEEE-style specials: exponent
+    field 0 is subnormal ``2^-14 * m / 4``, exponent 31 is +-inf (m == 0) or
+    NaN.  The reference's Triton path accepts float8_e5m2 caches and
+    dequantises them as ``code.to(float32) * scale``
+    (``integrations/vllm/l20_paged_split_kv.py:188-199,617-621``).
+    """
+    table = np.empty(256, dtype=np.float32)
+    for code in range(256):
+        sign = -1.0 if code & 0x80 else 1.0
+        exponent = (code >> 2) & 0x1F
+        mantissa = code & 0x3
+        if exponent == 0x1F:
+            table[code] = sign * np.inf if mantissa == 0 else np.nan
+        elif exponent == 0:
+            table[code] = sign * math.ldexp(mantissa / 4.0, -14)
+        else:
+            table[code] = sign * math.ldexp(1.0 + mantissa / 4.0, exponent - 15)
+    return table
+
+
+_DECODE_E5M2 = e5m2_decode_table()
+KV_FORMATS = ("e4m3fn", "e5m2")
+
+
+def decode_table(kv_format: str = "e4m3fn") -> np.ndarray:
+    """The 256-entry decode table of ``kv_format`` ("e4m3fn" or "e5m2")."""
+    if kv_format == "e4m3fn":
+        return _DECODE
+    if kv_format == "e5m2":
+        return _DECODE_E5M2
+    raise ValueError(f"unknown fp8 format {kv_format!r}")
+
+
+def fp8_to_f32(codes: np.ndarray, kv_format: str = "e4m3fn") -> np.ndarray:
+    """Decode uint8 codes of ``kv_format`` to float32 (exact)."""
+    return decode_table(kv_format)[np.asarray(codes, dtype=np.uint8)]
 
 
 def encode_e4m3fn(values: np.ndarray) -> np.ndarray:
@@ -166,9 +210,9 @@ def gather_pages(cache: np.ndarray, table_row: np.ndarray, length: int) -> np.nd
     return cache[physical, token % PAGE_SIZE]
 
 
-def dequantize(codes: np.ndarray, scale: ScaleLike, head_axis: int = -2) -> np.ndarray:
+def dequantize(codes: np.ndarray, scale: ScaleLike, head_axis: int = -2, kv_format: str = "e4m3fn") -> np.ndarray:
     """fp32 ``code * scale`` (one rounding), per tensor or per KV head."""
-    values = e4m3fn_to_f32(codes)
+    values = fp8_to_f32(codes, kv_format)
     heads = values.shape[head_axis]
     scales = _head_scales(scale, heads)
     shape = [1] * values.ndim
@@ -261,11 +305,12 @@ def reference(
     rows: Optional[Sequence[int]] = None,
     page_indptr: Optional[np.ndarray] = None,
     tree_mask: Optional[np.ndarray] = None,
+    kv_format: str = "e4m3fn",
 ) -> Tuple[np.ndarray, np.ndarray]:
     """Dequantise-then-attend (``smoke_cuda_paged_fp8_decode_op.py:22-41``).
 
     query       [B*q_len, Hq, D] float (bf16/fp16 values held as float32)
-    key/value   [P, 16, Hkv, D] uint8 e4m3fn codes
+    key/value   [P, 16, Hkv, D] uint8 codes of ``kv_format`` (e4m3fn or e5m2)
     block_table [B, max_pages] int (or the flat page list with ``page_indptr`` [B+1])
     seq_lens    [B] int;  k/v_scale float or [Hkv]
     Row ``b*q_len + i`` attends to keys ``0 .. L_b - q_len + i``.
@@ -287,8 +332,8 @@ def reference(
         if length <= 0:
             continue
         pages = table_row(block_table, b, page_indptr)
-        keys = dequantize(gather_pages(key_cache, pages, length), k_scale)
-        values = dequantize(gather_pages(value_cache, pages, length), v_scale)
+        keys = dequantize(gather_pages(key_cache, pages, length), k_scale, kv_format=kv_format)
+        values = dequantize(gather_pages(value_cache, pages, length), v_scale, kv_format=kv_format)
         if round_kv_to is not None:
             keys = keys.astype(round_kv_to).astype(np.float32)
             values = values.astype(round_kv_to).astype(np.float32)
@@ -348,6 +393,7 @@ def split_reference(
     *,
     softmax_scale: Optional[float] = None,
     q_len: int = 1,
+    kv_format: str = "e4m3fn",
 ) -> Tuple[np.ndarray, np.ndarray]:
     """Split-KV partials and LSE merge in float64 (``l20_paged_decode.cu:291-463``).
 
@@ -367,8 +413,10 @@ def split_reference(
         length = int(seq_lens[b])
         if length <= 0:
             continue
-        keys = dequantize(gather_pages(key_cache, block_table[b], length), k_scale).astype(np.float64)
-        values = dequantize(gather_pages(value_cache, block_table[b], length), v_scale).astype(np.float64)
+        keys = dequantize(gather_pages(key_cache, block_table[b], length), k_scale,
+                          kv_format=kv_format).astype(np.float64)
+        values = dequantize(gather_pages(value_cache, block_table[b], length), v_scale,
+                            kv_format=kv_format).astype(np.float64)
         kv_of_head = np.arange(num_q_heads) // group
         for i in range(q_len):
             r = b * q_len + i
@@ -409,6 +457,7 @@ def brute_force_fp64(
     softmax_scale: Optional[float] = None,
     q_len: int = 1,
     tree_mask: Optional[np.ndarray] = None,
+    kv_format: str = "e4m3fn",
 ) -> Tuple[np.ndarray, np.ndarray]:
     """Scalar float64 loops, written independently of ``reference``; tiny inputs only."""
     n_rows, num_q_heads, head_dim = np.asarray(query).shape
@@ -417,7 +466,7 @@ def brute_force_fp64(
     ks = _head_scales(k_scale, num_kv_heads)
     vs = _head_scales(v_scale, num_kv_heads)
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
-    decode = [float(v) for v in e4m3fn_decode_table()]
+    decode = [float(v) for v in (e4m3fn_decode_table() if kv_format == "e4m3fn" else e5m2_decode_table())]
     out = np.zeros((n_rows, num_q_heads, head_dim))
     lse = np.full((n_rows, num_q_heads), -np.inf)
     for r in range(n_rows):

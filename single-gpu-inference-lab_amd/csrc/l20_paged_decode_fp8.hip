@@ -124,26 +124,47 @@ template <typename QT> struct MfmaTypes;
 template <> struct MfmaTypes<__bf16> { typedef bf16x8 vec8; };
 template <> struct MfmaTypes<_Float16> { typedef f16x8 vec8; };
 
-// Eight e4m3fn codes (two dwords) -> eight bf16 / f16 MFMA operand elements,
-// exact (every e4m3fn value is representable in both).  gfx950
-// v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1.0, word_sel picking bytes
-// 0-1 or 2-3.  The pairs are moved as whole 32-bit words: per-lane extraction
-// of these conversions' results is miscompiled by the ROCm 7.2 LLVM.
-template <typename V8> __device__ __forceinline__ V8 fp8x8_to(int w0, int w1);
-template <> __device__ __forceinline__ bf16x8 fp8x8_to<bf16x8>(int w0, int w1) {
-  const i32x4 r = {
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+// Eight fp8 codes (two dwords) -> eight bf16 / f16 MFMA operand elements,
+// exact (every e4m3fn and every e5m2 value is representable in both).
+// gfx950 v_cvt_scalef32_pk_{bf16,f16}_{fp8,bf8} (fp8 = OCP e4m3, bf8 = OCP
+// e5m2) with scale 1.0, word_sel picking bytes 0-1 or 2-3.  The pairs are
+// moved as whole 32-bit words: per-lane extraction of these conversions'
+// results is miscompiled by the ROCm 7.2 LLVM.
+template <bool E5M2> __device__ __forceinline__ int cvt_pk_bf16(int w, bool hi) {
+  if constexpr (E5M2)
+    return hi ? __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true))
+              : __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false));
+  else
+    return hi ? __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
+              : __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+template <bool E5M2> __device__ __forceinline__ int cvt_pk_f16(int w, bool hi) {
+  if constexpr (E5M2)
+    return hi ? __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true))
+              : __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false));
+  else
+    return hi ? __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+              : __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+template <typename V8, bool E5M2> __device__ __forceinline__ V8 fp8x8_to(int w0, int w1);
+template <> __device__ __forceinline__ bf16x8 fp8x8_to<bf16x8, false>(int w0, int w1) {
+  const i32x4 r = {cvt_pk_bf16<false>(w0, false), cvt_pk_bf16<false>(w0, true), cvt_pk_bf16<false>(w1, false),
+                   cvt_pk_bf16<false>(w1, true)};
   return __builtin_bit_cast(bf16x8, r);
 }
-template <> __device__ __forceinline__ f16x8 fp8x8_to<f16x8>(int w0, int w1) {
-  const i32x4 r = {
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
-      __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+template <> __device__ __forceinline__ bf16x8 fp8x8_to<bf16x8, true>(int w0, int w1) {
+  const i32x4 r = {cvt_pk_bf16<true>(w0, false), cvt_pk_bf16<true>(w0, true), cvt_pk_bf16<true>(w1, false),
+                   cvt_pk_bf16<true>(w1, true)};
+  return __builtin_bit_cast(bf16x8, r);
+}
+template <> __device__ __forceinline__ f16x8 fp8x8_to<f16x8, false>(int w0, int w1) {
+  const i32x4 r = {cvt_pk_f16<false>(w0, false), cvt_pk_f16<false>(w0, true), cvt_pk_f16<false>(w1, false),
+                   cvt_pk_f16<false>(w1, true)};
+  return __builtin_bit_cast(f16x8, r);
+}
+template <> __device__ __forceinline__ f16x8 fp8x8_to<f16x8, true>(int w0, int w1) {
+  const i32x4 r = {cvt_pk_f16<true>(w0, false), cvt_pk_f16<true>(w0, true), cvt_pk_f16<true>(w1, false),
+                   cvt_pk_f16<true>(w1, true)};
   return __builtin_bit_cast(f16x8, r);
 }
 
@@ -155,8 +176,11 @@ __device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, f32x4 c)
 }
 
 // Byte pair (sel=0: bytes 0,1; sel=1: bytes 2,3) of a dword -> two f32.
-__device__ __forceinline__ f32x2 fp8x2_f32(int w, bool hi) {
-  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+template <bool E5M2> __device__ __forceinline__ f32x2 fp8x2_f32(int w, bool hi) {
+  if constexpr (E5M2)
+    return hi ? __builtin_amdgcn_cvt_pk_f32_bf8(w, true) : __builtin_amdgcn_cvt_pk_f32_bf8(w, false);
+  else
+    return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
 }
 
 template <typename QT> __device__ __forceinline__ QT from_f32(float x);
@@ -195,8 +219,9 @@ template <> struct BlockRaw16<64> {
   i32x4 k[2];
   i32x2 v[4];  // 4 elements at d = 4*(lane%16)
 };
-// KT = 0: e4m3fn codes, 32-token blocks; KT = 1: 16-bit elements of the MFMA
-// type, 16-token blocks (the same bytes per register buffer).
+// KT = 0: e4m3fn codes, 32-token blocks; KT = 2: e5m2 codes, the same; KT =
+// 1: 16-bit elements of the MFMA type, 16-token blocks (the same bytes per
+// register buffer).
 template <int KT, int D> struct KvBlock { typedef BlockRaw<D> type; };
 template <int D> struct KvBlock<1, D> { typedef BlockRaw16<D> type; };
 
@@ -296,9 +321,9 @@ struct KvUnit {
   typedef typename KvBlock<KT, D>::type Block;
   // Softmax probabilities: f16 for fp8 caches (V converted to f16), the
   // cache's own type for 16-bit caches.
-  typedef typename std::conditional<KT == 0, _Float16, QT>::type PT;
+  typedef typename std::conditional<KT != 1, _Float16, QT>::type PT;
   typedef typename MfmaTypes<PT>::vec8 pvec8;
-  static constexpr int kTok = KT == 0 ? 32 : 16;  // tokens per block
+  static constexpr int kTok = KT != 1 ? 32 : 16;  // tokens per block
   // P is rounded to the MFMA operand type, 11 significant bits (f16) or 8
   // (bf16), while the softmax denominator sums it unrounded.  Equal scores
   // round alike, so the error does not average out: with every other key at
@@ -446,9 +471,9 @@ struct KvUnit {
     // contributes exactly 0.  K needs no fix-up: their scores are replaced by
     // -inf below.  A 16-bit block has one tile; its second-tile slots are
     // empty (score -inf, V zero).
-    const bool bad0 = __builtin_amdgcn_readlane(pid, KT == 0 ? 2 * blk : blk) < 0;
-    const bool bad1 = KT == 0 ? __builtin_amdgcn_readlane(pid, 2 * blk + 1) < 0 : true;
-    if constexpr (KT == 0) {
+    const bool bad0 = __builtin_amdgcn_readlane(pid, KT != 1 ? 2 * blk : blk) < 0;
+    const bool bad1 = KT != 1 ? __builtin_amdgcn_readlane(pid, 2 * blk + 1) < 0 : true;
+    if constexpr (KT != 1) {
       if (tok0 + 32 > uEnd || bad0 || bad1) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -481,13 +506,13 @@ struct KvUnit {
       sc[qt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
       sc[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    if constexpr (KT == 0) {
+    if constexpr (KT != 1) {
 #pragma unroll
       for (int T = 0; T < 2; ++T) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           const i32x4 raw = r.k[T][s >> 1];
-          const qvec8 kop = fp8x8_to<qvec8>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
+          const qvec8 kop = fp8x8_to<qvec8, KT == 2>(raw[2 * (s & 1)], raw[2 * (s & 1) + 1]);
 #pragma unroll
           for (int qt = 0; qt < NQT; ++qt) sc[qt][T] = mfma16(kop, qop[qt][s], sc[qt][T]);
         }
@@ -574,7 +599,7 @@ struct KvUnit {
 #pragma unroll
     for (int tp2 = 0; tp2 < NT; tp2 += 2) {
       i32x4 wa, wb;
-      if constexpr (KT == 0) {
+      if constexpr (KT != 1) {
         // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
@@ -586,8 +611,8 @@ struct KvUnit {
             w0 = r.v[e];
             w1 = r.v[e + 1];
           }
-          const f32x2 f0 = fp8x2_f32(w0, (tp2 & 3) != 0);
-          const f32x2 f1 = fp8x2_f32(w1, (tp2 & 3) != 0);
+          const f32x2 f0 = fp8x2_f32<KT == 2>(w0, (tp2 & 3) != 0);
+          const f32x2 f1 = fp8x2_f32<KT == 2>(w1, (tp2 & 3) != 0);
           wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
           wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
         }
@@ -782,7 +807,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   auto n_blocks = [&](int s, int L) {
     const int start = s * S;
     const int tiles = max(0, (min(start + S, L) - start + kPage - 1) / kPage);
-    return KT == 0 ? (tiles + 1) >> 1 : tiles;
+    return KT != 1 ? (tiles + 1) >> 1 : tiles;
   };
   // Sequence b's page list and its length (a block-table row, or the CSR
   // slice; l20_paged_decode.cu:205-208).
@@ -841,7 +866,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     if (cs < splits_of_len(cL, S)) {
       const int tiles = max(0, (min(start + S, cL) - start + kPage - 1) / kPage);
       pidU = (lane < tiles && lane < spec && v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
-      const int nU = KT == 0 ? (tiles + 1) >> 1 : tiles;
+      const int nU = KT != 1 ? (tiles + 1) >> 1 : tiles;
       if (nU > 0) load_block(buf[0], pidU, wave, 0);
       if constexpr (NB > 1)
         if (nU > 1) load_block(buf[NB - 1], pidU, wave, 1);
@@ -1479,8 +1504,8 @@ __global__ void dequant_f32_kernel(const uint8_t *src, float *dst, int64_t n, fl
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
   const int w = load_codes4(src, i, n);
-  const f32x2 lo = fp8x2_f32(w, false);
-  const f32x2 hi = fp8x2_f32(w, true);
+  const f32x2 lo = fp8x2_f32<false>(w, false);
+  const f32x2 hi = fp8x2_f32<false>(w, true);
   const float v[4] = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -1492,7 +1517,7 @@ __global__ void dequant_bf16_kernel(const uint8_t *src, uint16_t *dst, int64_t n
   if (i >= n) return;
   const int w = load_codes4(src, i, n);
   // Same conversion as the attention kernel's K operand; words, not lanes.
-  const i32x4 both = __builtin_bit_cast(i32x4, fp8x8_to<bf16x8>(w, 0));
+  const i32x4 both = __builtin_bit_cast(i32x4, fp8x8_to<bf16x8, false>(w, 0));
   const uint32_t lo = (uint32_t)both[0];
   const uint32_t hi = (uint32_t)both[1];
   if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(dst + i) & 7) == 0)) {
@@ -1557,9 +1582,10 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (!a) return fail(L20_PD_EINVAL, "null argument block");
   if (a->query_dtype != L20_PD_BF16 && a->query_dtype != L20_PD_FP16)
     return fail(L20_PD_EINVAL, "query must be bf16 or fp16");
-  if (a->kv_dtype != L20_PD_KV_FP8_E4M3 && a->kv_dtype != L20_PD_KV_FP16 && a->kv_dtype != L20_PD_KV_BF16)
+  if (a->kv_dtype != L20_PD_KV_FP8_E4M3 && a->kv_dtype != L20_PD_KV_FP16 && a->kv_dtype != L20_PD_KV_BF16 &&
+      a->kv_dtype != L20_PD_KV_FP8_E5M2)
     return fail(L20_PD_EINVAL, "unknown K/V cache dtype");
-  const bool kv16 = a->kv_dtype != L20_PD_KV_FP8_E4M3;
+  const bool kv16 = a->kv_dtype == L20_PD_KV_FP16 || a->kv_dtype == L20_PD_KV_BF16;
   if (kv16 && (a->kv_dtype == L20_PD_KV_BF16) != (a->query_dtype == L20_PD_BF16))
     return fail(L20_PD_EINVAL, "query and 16-bit K/V cache must have the same dtype");
   const int64_t es = kv16 ? 2 : 1;  // bytes per cache element
@@ -1685,7 +1711,7 @@ hipError_t launch_partial_mask(const l20pd::PartialParams &pp, int head_dim, int
     // wave halves the bytes queued in the memory system at full bandwidth
     // (verify shape 130.7 -> 126.4 us per call, long context 106.1 -> 104.5);
     // shorter units keep two for the latency-bound end of the launch.
-    if constexpr (KT == 0)
+    if constexpr (KT != 1)
       if (pp.split_size >= 1024)
         return nqt == 1 ? launch_partial<QT, KT, 128, 1, TREE, 1>(pp, batch, num_kv_heads, stream)
                         : launch_partial<QT, KT, 128, 2, TREE, 1>(pp, batch, num_kv_heads, stream);
@@ -1760,7 +1786,7 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.q_srow = a.q_stride_row;
   pp.q_shead = a.q_stride_head;
   // The kernels address the caches in bytes.
-  const int64_t es = a.kv_dtype == L20_PD_KV_FP8_E4M3 ? 1 : 2;
+  const int64_t es = (a.kv_dtype == L20_PD_KV_FP16 || a.kv_dtype == L20_PD_KV_BF16) ? 2 : 1;
   pp.k = a.key_cache;
   pp.k_spage = a.k_stride_page * es;
   pp.k_stok32 = (int)(a.k_stride_token * es);
@@ -1908,7 +1934,8 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   g_last_error[0] = '\0';
   const int32_t rc = check_args(a);
   if (rc != L20_PD_OK) return rc;
-  const bool kv16 = a->kv_dtype != L20_PD_KV_FP8_E4M3;
+  const bool kv16 = a->kv_dtype == L20_PD_KV_FP16 || a->kv_dtype == L20_PD_KV_BF16;
+  const bool e5m2 = a->kv_dtype == L20_PD_KV_FP8_E5M2;
   if (!(kinds & (kv16 ? kKv16 : kKvFp8)))
     return fail(L20_PD_EINVAL, kv16 ? "K/V cache must be torch.float8_e4m3fn"
                                     : "K/V cache must be fp16 or bf16 for this entry point");
@@ -1928,6 +1955,9 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
     if (kv16)
       e = bf16 ? launch_partial_shape<__bf16, 1>(pp, D, nqt, B, H, stream)
                : launch_partial_shape<_Float16, 1>(pp, D, nqt, B, H, stream);
+    else if (e5m2)
+      e = bf16 ? launch_partial_shape<__bf16, 2>(pp, D, nqt, B, H, stream)
+               : launch_partial_shape<_Float16, 2>(pp, D, nqt, B, H, stream);
     else
       e = bf16 ? launch_partial_shape<__bf16, 0>(pp, D, nqt, B, H, stream)
                : launch_partial_shape<_Float16, 0>(pp, D, nqt, B, H, stream);

@@ -222,11 +222,16 @@ at::Tensor paged_decode_fp8_e4m3_split_out(
     const std::optional<at::Tensor> &k_scale_per_head, const std::optional<at::Tensor> &v_scale_per_head,
     int64_t q_len, const std::optional<at::Tensor> &lse, const std::optional<at::Tensor> &tree_mask) {
   check_query(query);
-  TORCH_CHECK(key_cache.scalar_type() == at::kFloat8_e4m3fn && value_cache.scalar_type() == at::kFloat8_e4m3fn,
-              "K/V cache must be torch.float8_e4m3fn");
+  // e4m3fn as in the reference's CUDA op; e5m2 as its Triton path accepts
+  // (integrations/vllm/l20_paged_split_kv.py:617-621).
+  const bool e5m2 = key_cache.scalar_type() == at::kFloat8_e5m2;
+  TORCH_CHECK((key_cache.scalar_type() == at::kFloat8_e4m3fn || e5m2) &&
+                  value_cache.scalar_type() == key_cache.scalar_type(),
+              "K/V cache must be torch.float8_e4m3fn (or both torch.float8_e5m2)");
   l20_pd_fp8_args a = make_args(query, key_cache, value_cache, PageTable{&block_table, nullptr}, seq_lens,
                                 partial_output, partial_max, partial_sum, output, max_seq_len, split_size,
-                                softmax_scale, q_len, lse, L20_PD_KV_FP8_E4M3, tree_mask);
+                                softmax_scale, q_len, lse, e5m2 ? L20_PD_KV_FP8_E5M2 : L20_PD_KV_FP8_E4M3,
+                                tree_mask);
   for (int which = 0; which < 2; ++which) {
     const auto &opt = which == 0 ? k_scale_per_head : v_scale_per_head;
     if (opt.has_value() && opt->defined()) {

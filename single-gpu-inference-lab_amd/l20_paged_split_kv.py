@@ -14,7 +14,8 @@ Differences: any split size the op accepts (multiple of 16 in [64, 1024]),
 no cap on the split count, an fp32 partial workspace with exactly
 ``ceil(max_seq_len / split_size)`` splits, bf16/fp16 queries, head_dim 64 or
 128, per-head scales, ``q_len > 1`` (causal among the new tokens) and an
-optional fp32 LSE output.  Strided K/V views (vLLM's ``kv_cache.unbind(1)``)
+optional fp32 LSE output.  Caches are float8_e4m3fn or float8_e5m2, as the
+reference's dtype check allows (``:617-621``).  Strided K/V views (vLLM's ``kv_cache.unbind(1)``)
 are honoured.
 """
 
@@ -97,8 +98,8 @@ def l20_paged_split_kv_attention_fp8(
         raise RuntimeError("requires an MI355X (gfx950) GPU")
     if query.ndim != 3 or key_cache.ndim != 4 or value_cache.shape != key_cache.shape:
         raise RuntimeError("expected Q=[B,H,D], cache=[pages,page,Hkv,D]")
-    if key_cache.dtype != torch.float8_e4m3fn or value_cache.dtype != key_cache.dtype:
-        raise RuntimeError("key/value cache must use a torch FP8 dtype (float8_e4m3fn)")
+    if key_cache.dtype not in (torch.float8_e4m3fn, torch.float8_e5m2) or value_cache.dtype != key_cache.dtype:
+        raise RuntimeError("key/value cache must use a torch FP8 dtype")
     rows, num_q_heads, head_dim = query.shape
     _, page_size, num_kv_heads, cache_dim = key_cache.shape
     batch = rows // q_len if q_len > 0 else -1

@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).with_name("libl20_paged_decode_hip.so")
 
 L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
 L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
-L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16 = 0, 1, 2
+L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16, L20_PD_KV_FP8_E5M2 = 0, 1, 2, 3
 L20_PD_DEVERR_PREFIX_WAIT, L20_PD_DEVERR_ACK_WAIT, L20_PD_DEVERR_PUBLISH_WAIT = 1, 2, 4
 ABI_VERSION = 3
 
@@ -156,6 +156,8 @@ def _kv_code(t) -> int:
         return L20_PD_KV_FP16
     if t.dtype == torch.bfloat16:
         return L20_PD_KV_BF16
+    if t.dtype == torch.float8_e5m2:
+        return L20_PD_KV_FP8_E5M2
     return L20_PD_KV_FP8_E4M3
 
 
@@ -165,7 +167,7 @@ def args_from_tensors(query, key_cache, value_cache, block_table, seq_lens, part
                       page_indptr=None, tree_mask=None) -> L20PdFp8Args:
     """Fill ``l20_pd_fp8_args`` from tensors (same argument order as the fp8 op).
 
-    The cache dtype picks ``kv_dtype`` (fp8 e4m3fn, fp16 or bf16).  With
+    The cache dtype picks ``kv_dtype`` (fp8 e4m3fn or e5m2, fp16 or bf16).  With
     ``page_indptr`` [B+1], ``block_table`` is the flat CSR page list.
 
     The struct holds raw device pointers; it also keeps a reference to every
@@ -231,7 +233,8 @@ def _call(name: str, args: L20PdFp8Args, stream: int, lib: Optional[ctypes.CDLL]
 def split_out(args: L20PdFp8Args, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
     """Call ``l20_pd_fp8_e4m3_split_out`` (fp8 caches) or ``l20_pd_split_out`` (16-bit
     caches); raise RuntimeError with the library's message on failure."""
-    name = "l20_pd_fp8_e4m3_split_out" if args.kv_dtype == L20_PD_KV_FP8_E4M3 else "l20_pd_split_out"
+    fp8 = args.kv_dtype in (L20_PD_KV_FP8_E4M3, L20_PD_KV_FP8_E5M2)
+    name = "l20_pd_fp8_e4m3_split_out" if fp8 else "l20_pd_split_out"
     _call(name, args, stream, lib)
 
 

@@ -28,9 +28,30 @@ COS_MIN = 0.9999
 LSE_RTOL = 1e-4
 
 
+def quantize_e5m2(raw, per_head_axis=None):
+    """OCP e5m2 codes of ``raw`` with the e4m3 quantiser's rule scaled to e5m2's
+    largest finite value 57344: ``scale = max(amax / 57344, 1e-12)``."""
+    xf = raw.float()
+    if per_head_axis is None:
+        scale = max(float(xf.abs().max()) / 57344.0, 1e-12)
+        return (xf / scale).clamp(-57344.0, 57344.0).to(torch.float8_e5m2), scale
+    moved = xf.movedim(per_head_axis, 0)
+    scales = torch.clamp(moved.reshape(moved.shape[0], -1).abs().amax(dim=1) / 57344.0, min=1e-12)
+    shape = [1] * xf.dim()
+    shape[per_head_axis] = -1
+    return (xf / scales.view(shape)).clamp(-57344.0, 57344.0).to(torch.float8_e5m2), scales
+
+
+def kv_format(cache) -> str:
+    """Oracle name of an fp8 cache's format."""
+    return "e5m2" if cache.dtype == torch.float8_e5m2 else "e4m3fn"
+
+
 def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, device="cuda",
-                   dtype=torch.bfloat16, pool_extra=7, max_pages=None, garbage_tail=False):
-    """Seeded paged inputs of an arbitrary shape (generated on CPU, copied to ``device``)."""
+                   dtype=torch.bfloat16, pool_extra=7, max_pages=None, garbage_tail=False, fp8="e4m3fn"):
+    """Seeded paged inputs of an arbitrary shape (generated on CPU, copied to ``device``).
+
+    ``fp8`` picks the cache format: "e4m3fn" (the reference's quantiser) or "e5m2"."""
     import l20_pd_workloads as wl
 
     g = torch.Generator().manual_seed(seed)
@@ -49,7 +70,10 @@ def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, 
     caches = []
     for _ in range(2):
         raw = torch.randn(pool, 16, hkv, d, generator=g).to(torch.bfloat16)
-        codes, scale = wl.quantize_fp8_e4m3(raw, per_head_axis=2 if per_head else None)
+        if fp8 == "e5m2":
+            codes, scale = quantize_e5m2(raw, per_head_axis=2 if per_head else None)
+        else:
+            codes, scale = wl.quantize_fp8_e4m3(raw, per_head_axis=2 if per_head else None)
         if garbage_tail:
             # bytes beyond each sequence's end in its last page: NaN codes
             u8 = codes.view(torch.uint8)
@@ -131,7 +155,8 @@ def run_oracle(inp, rows: Optional[Sequence[int]] = None):
         inp["block_table"].cpu().numpy(),
         inp["seq_lens"].cpu().numpy(),
         host_scale(inp["k_scale"]), host_scale(inp["v_scale"]),
-        softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows, tree_mask=_host_tree(inp))
+        softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows, tree_mask=_host_tree(inp),
+        kv_format=kv_format(inp["key_cache"]))
 
 
 def compare(out, lse, exp_out, exp_lse, rows: Optional[np.ndarray] = None, check_lse=True):

@@ -501,3 +501,100 @@ def test_fp8_op_rejects_16bit_caches_and_vice_versa():
         torch.ops.l20_stack.paged_decode_split_out(
             fp8["query"], fp8["key_cache"], fp8["value_cache"], fp8["block_table"], fp8["seq_lens"], po, pm, ps,
             torch.empty_like(fp8["query"]), fp8["max_seq_len"], 64)
+
+
+# ------------------------------------------------------------ OCP e5m2 caches
+# The reference's hook-facing Triton op accepts float8_e5m2 caches
+# (integrations/vllm/l20_paged_split_kv.py:617-621) and dequantises them as
+# code * scale like e4m3fn ones.
+E5M2 = [
+    # name, batch, hq, hkv, d, lens, q_len, per_head, dtype
+    ("ragged_d128", 5, 28, 4, 128, [1, 15, 16, 33, 1025], 1, False, torch.bfloat16),
+    ("ragged_d64_per_head", 5, 14, 2, 64, [1, 15, 16, 17, 500], 1, True, torch.float16),
+    ("empty_seq", 3, 8, 2, 128, [0, 40, 0], 1, False, torch.bfloat16),
+    ("verify_q4", 3, 16, 2, 128, [70, 4, 513], 4, False, torch.bfloat16),
+    ("long_gqa7", 2, 28, 4, 128, [4096, 2500], 1, False, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", E5M2, ids=[c[0] for c in E5M2])
+@pytest.mark.parametrize("split", [64, 512])
+@pytest.mark.parametrize("via", ["torch", "cabi"])
+def test_e5m2_caches(case, split, via):
+    _, batch, hq, hkv, d, lens, q_len, per_head, dtype = case
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, per_head=per_head, dtype=dtype, fp8="e5m2",
+                           seed=zlib.crc32(case[0].encode()) % 1000, garbage_tail=True)
+    assert inp["key_cache"].dtype == torch.float8_e5m2
+    exp = H.run_oracle(inp)
+    H.compare(*H.run_op(inp, split, via=via), *exp)
+
+
+def test_e5m2_every_finite_code_end_to_end():
+    """V: 248 one-token sequences, sequence c's value row all code c: the output
+    (fp16, which holds every e5m2 value) is the code's value exactly.  K: 248
+    two-token sequences, key 0 = code c on dim 0, key 1 = 0, query = e_0 with
+    softmax scale 1: the LSE is log(1 + exp(value(c)))."""
+    from oracle import paged_fp8_decode_ref as ref
+
+    table = ref.e5m2_decode_table()
+    codes = np.array([c for c in range(256) if np.isfinite(table[c])], dtype=np.uint8)
+    n, d = len(codes), 128
+    assert n == 248
+    vc = torch.zeros(n + 1, 16, 1, d, dtype=torch.uint8)
+    vc[:n, 0, 0, :] = torch.from_numpy(codes)[:, None]
+    kc = torch.zeros(n + 1, 16, 1, d, dtype=torch.uint8)
+    kc[:n, 0, 0, 0] = torch.from_numpy(codes)
+    vk = torch.zeros_like(vc)
+    vk[:n, 0, 0, :] = 0x3C  # e5m2 1.0: out = softmax weight of key 0
+    query = torch.zeros(n, 1, d, dtype=torch.float16)
+    query[:, 0, 0] = 1.0
+    table_t = torch.arange(n, dtype=torch.int32).view(n, 1)
+    base = {"query": query.cuda(), "block_table": table_t.cuda(), "k_scale": 1.0, "v_scale": 1.0,
+            "softmax_scale": 1.0, "q_len": 1}
+    v_case = dict(base, key_cache=torch.zeros_like(vc).view(torch.float8_e5m2).cuda(),
+                  value_cache=vc.view(torch.float8_e5m2).cuda(),
+                  seq_lens=torch.ones(n, dtype=torch.int32).cuda(), max_seq_len=1)
+    out, _ = H.run_op(v_case, 64)
+    want = table[codes]
+    got = out[:, 0, :].float().cpu().numpy()
+    assert np.array_equal(got, np.broadcast_to(want[:, None], got.shape))
+    k_case = dict(base, key_cache=kc.view(torch.float8_e5m2).cuda(), value_cache=vk.view(torch.float8_e5m2).cuda(),
+                  seq_lens=torch.full((n,), 2, dtype=torch.int32).cuda(), max_seq_len=2)
+    _, lse = H.run_op(k_case, 64)
+    exact = np.logaddexp(table[codes].astype(np.float64), 0.0)
+    got_lse = lse[:, 0].cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got_lse, exact, rtol=2e-6, atol=2e-5)
+
+
+def test_e5m2_hook_api_and_noalloc():
+    import l20_pd_cabi as cabi
+    from l20_paged_split_kv import allocate_l20_paged_split_kv_workspace, l20_paged_split_kv_attention_fp8
+
+    inp = H.make_synthetic(4, 28, 4, 128, [3000, 700, 64, 1500], fp8="e5m2", seed=33)
+    exp = H.run_oracle(inp)
+    ws = allocate_l20_paged_split_kv_workspace(inp["query"], inp["max_seq_len"], split_size=512)
+    out = l20_paged_split_kv_attention_fp8(inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                           inp["seq_lens"], k_scale=inp["k_scale"], v_scale=inp["v_scale"],
+                                           max_seq_len=inp["max_seq_len"], split_size=512, workspace=ws)
+    torch.cuda.synchronize()
+    H.compare(out, None, exp[0], exp[1], check_lse=False)
+    out2 = torch.empty_like(inp["query"])
+    lse2 = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+    po, pm, ps = H.workspace(inp, 512)
+    args = cabi.args_from_tensors(inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                  inp["seq_lens"], po, pm, ps, out2, inp["k_scale"], inp["v_scale"],
+                                  inp["max_seq_len"], 512, softmax_scale=inp["softmax_scale"], lse=lse2)
+    assert args.kv_dtype == cabi.L20_PD_KV_FP8_E5M2
+    cabi.split_out_noalloc(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    H.compare(out2, lse2, *exp)
+
+
+def test_mixed_fp8_formats_are_rejected():
+    inp = H.make_synthetic(2, 8, 2, 128, [40, 20], seed=1)
+    v5 = inp["value_cache"].float().to(torch.float8_e5m2)
+    po, pm, ps = H.workspace(inp, 64)
+    with pytest.raises(RuntimeError, match="float8"):
+        torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
+            inp["query"], inp["key_cache"], v5, inp["block_table"], inp["seq_lens"], po, pm, ps,
+            torch.empty_like(inp["query"]), 1.0, 1.0, inp["max_seq_len"], 64)

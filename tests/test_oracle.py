@@ -67,6 +67,53 @@ def test_quantize_matches_torch_workload_quantizer():
     assert np.array_equal(codes_t.view(torch.uint8).numpy(), codes_n)
 
 
+def test_e5m2_decode_table_matches_torch_and_fp16_top_byte():
+    table = ref.e5m2_decode_table()
+    codes = torch.arange(256, dtype=torch.uint8)
+    via_torch = codes.view(torch.float8_e5m2).float().numpy()
+    # e5m2 is fp16 with the low 8 mantissa bits dropped
+    via_fp16 = (codes.to(torch.int16) << 8).view(torch.float16).float().numpy()
+    nan = np.isnan(table)
+    assert np.array_equal(np.flatnonzero(nan), [0x7D, 0x7E, 0x7F, 0xFD, 0xFE, 0xFF])
+    for other in (via_torch, via_fp16):
+        assert np.array_equal(np.isnan(other), nan)
+        assert np.array_equal(table[~nan], other[~nan])
+        assert np.array_equal(np.signbit(table[~nan]), np.signbit(other[~nan]))
+    assert table[0x7C] == np.inf and table[0xFC] == -np.inf
+    assert table[0x01] == 2.0 ** -16 and table[0x04] == 2.0 ** -14 and table[0x3C] == 1.0
+    assert table[0x7B] == 57344.0
+    assert np.array_equal(ref.fp8_to_f32(np.array([0x3C, 0xBC]), "e5m2"), [1.0, -1.0])
+    with pytest.raises(ValueError):
+        ref.decode_table("e4m3fnuz")
+
+
+def _e5m2_case(seed, batch, hq, hkv, d, lens, q_len=1):
+    """make_case's layout with e5m2 codes (via torch's float8_e5m2 rounding)."""
+    case = make_case(seed, batch, hq, hkv, d, lens, q_len=q_len)
+    rng = np.random.default_rng(seed + 100)
+    for name in ("key_cache", "value_cache"):
+        raw = torch.from_numpy(rng.standard_normal(case[name].shape).astype(np.float32) * 300)
+        case[name] = raw.to(torch.float8_e5m2).view(torch.uint8).numpy()
+    case["k_scale"], case["v_scale"] = 0.01, 0.003
+    return case
+
+
+@pytest.mark.parametrize("spec", [dict(seed=5, batch=2, hq=4, hkv=2, d=64, lens=[17, 33]),
+                                  dict(seed=6, batch=2, hq=4, hkv=2, d=64, lens=[21, 9], q_len=4)])
+def test_e5m2_reference_matches_brute_force_and_split(spec):
+    case = _e5m2_case(**spec)
+    out, lse = run(ref.reference, case, kv_format="e5m2")
+    out64, lse64 = run(ref.brute_force_fp64, case, kv_format="e5m2")
+    np.testing.assert_allclose(out, out64, atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(lse, lse64, atol=2e-6, rtol=1e-6)
+    out_s, lse_s = run(ref.split_reference, case, split_size=16, kv_format="e5m2")
+    np.testing.assert_allclose(out_s, out64, atol=1e-5)
+    np.testing.assert_allclose(lse_s, lse64, atol=1e-5)
+    # the same bytes read as e4m3fn give a different answer: the format switch is live
+    out_wrong, _ = run(ref.reference, case)
+    assert not np.allclose(out_wrong, out, atol=1e-3, equal_nan=True)
+
+
 # ---------------------------------------------------------------- helpers
 def make_case(seed, batch, hq, hkv, d, lens, q_len=1, per_head=False, pool_extra=3):
     rng = np.random.default_rng(seed)
