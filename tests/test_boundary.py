@@ -52,10 +52,12 @@ def test_num_splits_and_default_split_size():
         split = lib.l20_pd_default_split_size(b, h, s, 256)
         assert 64 <= split <= 1024 and split % 16 == 0
     # long contexts take the largest split; serving batches the hook's 512;
-    # short contexts keep ~8 splits per sequence
+    # short contexts keep ~8 splits per sequence, and halve the split while the
+    # items fill at most half the grid (32 x 8 items on 1024 slots -> 128)
     assert lib.l20_pd_default_split_size(2, 8, 131072, 256) == 1024
     assert lib.l20_pd_default_split_size(128, 4, 8192, 256) == 512
-    assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 256
+    assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 128
+    assert lib.l20_pd_default_split_size(64, 2, 2048, 256) == 256
     assert lib.l20_pd_default_split_size(4, 2, 512, 256) == 64
     # doubled when that fits every item in one round of the persistent grid
     # (64 sequences x 4 splits on 256 one-workgroup CUs), never past 1024

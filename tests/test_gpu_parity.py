@@ -56,7 +56,7 @@ def test_fp8_conversions_match_oracle_table_on_all_codes():
 # ------------------------------------------------------------ the five configurations
 CONFIG_SPLITS = {
     "c1_qwen2.5_0.5b": [64, 512],
-    "c2_qwen2.5_coder_3b": [256, 1024],
+    "c2_qwen2.5_coder_3b": [128, 256, 1024],  # 128: the library default
     "c3_qwen2.5_7b": [512, 1024],
     "c4_llama3_8b_long": [1024],
     # 1024 is the library default for this shape (the two-tile, one-block-in-
