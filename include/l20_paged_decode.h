@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define L20_PD_ABI_VERSION 3
+#define L20_PD_ABI_VERSION 4
 
 /* Element types for query/output and the partial-output workspace. */
 enum l20_pd_dtype {

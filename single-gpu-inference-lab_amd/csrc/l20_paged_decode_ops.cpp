@@ -30,6 +30,7 @@
 
 #include "l20_kv_write.h"
 #include "l20_paged_decode.h"
+#include "l20_tree_verify.h"
 
 namespace {
 
@@ -408,6 +409,77 @@ void kv_fp8_scales(const at::Tensor &key, const at::Tensor &value, const at::Ten
   TORCH_CHECK(rc == L20_PD_OK, l20_pd_last_error());
 }
 
+// Draft-suffix attention merged with the paged prefix's result (the suffix and
+// merge launches of src/l20_stack/ops/triton_tree_attention.py:1152-1197).
+void tree_suffix_merge(const at::Tensor &query, const at::Tensor &suffix_key, const at::Tensor &suffix_value,
+                       const at::Tensor &ancestor_mask, const at::Tensor &prefix_output,
+                       const at::Tensor &prefix_lse, const at::Tensor &output, double softmax_scale) {
+  check_query(query);
+  TORCH_CHECK(query.dim() == 4, "expected query=[B,S,Hq,D]");
+  TORCH_CHECK(suffix_key.dim() == 4 && suffix_value.sizes() == suffix_key.sizes(),
+              "expected suffix key/value=[B,S,Hkv,D]");
+  TORCH_CHECK(suffix_key.scalar_type() == query.scalar_type() && suffix_value.scalar_type() == query.scalar_type(),
+              "suffix key/value must have the query's dtype");
+  TORCH_CHECK(suffix_key.size(0) == query.size(0) && suffix_key.size(1) == query.size(1) &&
+                  suffix_key.size(3) == query.size(3),
+              "suffix KV must match query batch/draft and cache kv heads");
+  TORCH_CHECK(ancestor_mask.dim() == 2 && ancestor_mask.size(0) == query.size(1) &&
+                  ancestor_mask.size(1) == query.size(1) &&
+                  (ancestor_mask.scalar_type() == at::kBool || ancestor_mask.scalar_type() == at::kByte),
+              "ancestor_mask must match draft_length");
+  TORCH_CHECK(prefix_output.sizes() == query.sizes() && output.sizes() == query.sizes(),
+              "prefix_output and output must be shaped like the query");
+  TORCH_CHECK(output.scalar_type() == query.scalar_type(), "output must have the query's dtype");
+  TORCH_CHECK(prefix_lse.scalar_type() == at::kFloat && prefix_lse.dim() == 3 &&
+                  prefix_lse.size(0) == query.size(0) && prefix_lse.size(1) == query.size(1) &&
+                  prefix_lse.size(2) == query.size(2),
+              "prefix_lse must be fp32 [B,S,Hq]");
+  for (const at::Tensor *t : {&query, &suffix_key, &suffix_value, &prefix_output, &output})
+    TORCH_CHECK(t->stride(3) == 1, "head_dim must be the contiguous dimension");
+  for (const at::Tensor *t : {&suffix_key, &suffix_value, &ancestor_mask, &prefix_output, &prefix_lse, &output})
+    check_same_device(*t, query, "every tensor");
+  l20_pd_tree_suffix_args a{};
+  a.query = query.data_ptr();
+  a.q_stride_batch = query.stride(0);
+  a.q_stride_draft = query.stride(1);
+  a.q_stride_head = query.stride(2);
+  a.query_dtype = dtype_code(query);
+  a.suffix_key = suffix_key.data_ptr();
+  a.sk_stride_batch = suffix_key.stride(0);
+  a.sk_stride_draft = suffix_key.stride(1);
+  a.sk_stride_head = suffix_key.stride(2);
+  a.suffix_value = suffix_value.data_ptr();
+  a.sv_stride_batch = suffix_value.stride(0);
+  a.sv_stride_draft = suffix_value.stride(1);
+  a.sv_stride_head = suffix_value.stride(2);
+  a.ancestor_mask = static_cast<const uint8_t *>(ancestor_mask.data_ptr());
+  a.mask_stride_row = ancestor_mask.stride(0);
+  a.mask_stride_col = ancestor_mask.stride(1);
+  a.prefix_output = prefix_output.data_ptr();
+  a.po_stride_batch = prefix_output.stride(0);
+  a.po_stride_draft = prefix_output.stride(1);
+  a.po_stride_head = prefix_output.stride(2);
+  a.prefix_dtype = dtype_code(prefix_output);
+  a.prefix_lse = prefix_lse.data_ptr<float>();
+  a.pl_stride_batch = prefix_lse.stride(0);
+  a.pl_stride_draft = prefix_lse.stride(1);
+  a.pl_stride_head = prefix_lse.stride(2);
+  a.output = output.data_ptr();
+  a.o_stride_batch = output.stride(0);
+  a.o_stride_draft = output.stride(1);
+  a.o_stride_head = output.stride(2);
+  a.softmax_scale = (float)softmax_scale;
+  a.batch = (int32_t)query.size(0);
+  a.draft_length = (int32_t)query.size(1);
+  a.num_q_heads = (int32_t)query.size(2);
+  a.num_kv_heads = (int32_t)suffix_key.size(2);
+  a.head_dim = (int32_t)query.size(3);
+  const c10::DeviceGuard guard(query.device());
+  void *stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.get_device()).stream();
+  const int32_t rc = l20_pd_tree_suffix_merge(&a, stream);
+  TORCH_CHECK(rc == L20_PD_OK, l20_pd_last_error());
+}
+
 }  // namespace
 
 TORCH_LIBRARY(l20_stack, m) {
@@ -449,6 +521,9 @@ TORCH_LIBRARY(l20_stack, m) {
       "kv_fp8_scales(Tensor key, Tensor value, Tensor positions, Tensor cos_sin_cache, bool is_neox, "
       "Tensor key_cache, Tensor value_cache, Tensor slot_mapping, Tensor(a!) k_scales, "
       "Tensor(b!) v_scales, bool per_head=True) -> ()");
+  m.def(
+      "tree_suffix_merge(Tensor query, Tensor suffix_key, Tensor suffix_value, Tensor ancestor_mask, "
+      "Tensor prefix_output, Tensor prefix_lse, Tensor(a!) output, float softmax_scale) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(l20_stack, CUDA, m) {
@@ -457,4 +532,5 @@ TORCH_LIBRARY_IMPL(l20_stack, CUDA, m) {
   m.impl("paged_decode_split_out", &paged_decode_split_out);
   m.impl("paged_decode_fp8_e4m3_split_out", &paged_decode_fp8_e4m3_split_out);
   m.impl("paged_decode_split_indices_out", &paged_decode_split_indices_out);
+  m.impl("tree_suffix_merge", &tree_suffix_merge);
 }

@@ -27,7 +27,7 @@ HIP_LIB = HERE / "libl20_paged_decode_hip.so"
 OPS_LIB = HERE / "l20_paged_decode_ops.so"
 ARCH = os.environ.get("L20_PD_ARCH", "gfx950")
 # The decode kernels and the paged KV-cache producer, one shared object.
-HIP_SOURCES = [CSRC / "l20_paged_decode_fp8.hip", CSRC / "l20_kv_write.hip"]
+HIP_SOURCES = [CSRC / "l20_paged_decode_fp8.hip", CSRC / "l20_kv_write.hip", CSRC / "l20_tree_suffix.hip"]
 
 # Packed-FP32 VALU forms are kept out of every HIP build.
 HIP_FLAGS = [

@@ -18,7 +18,7 @@ L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
 L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
 L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16, L20_PD_KV_FP8_E5M2 = 0, 1, 2, 3
 L20_PD_DEVERR_PREFIX_WAIT, L20_PD_DEVERR_ACK_WAIT, L20_PD_DEVERR_PUBLISH_WAIT = 1, 2, 4
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every extern "C" symbol declared in include/*.h.
 EXPORTED = (
@@ -41,6 +41,8 @@ EXPORTED = (
     "l20_pd_kv_write_check",
     "l20_pd_rope_and_cache",
     "l20_pd_kv_fp8_scales",
+    "l20_pd_tree_suffix_check",
+    "l20_pd_tree_suffix_merge",
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -68,6 +70,24 @@ class L20PdFp8Args(ctypes.Structure):
         ("max_seq_len", _i32), ("split_size", _i32),
         ("kv_dtype", _i32), ("page_indptr", _vp),
         ("tree_mask", _vp), ("tree_mask_stride_batch", _i64),
+    ]
+
+
+class L20PdTreeSuffixArgs(ctypes.Structure):
+    """Mirror of ``l20_pd_tree_suffix_args`` (include/l20_tree_verify.h)."""
+
+    _fields_ = [
+        ("query", _vp), ("q_stride_batch", _i64), ("q_stride_draft", _i64), ("q_stride_head", _i64),
+        ("query_dtype", _i32),
+        ("suffix_key", _vp), ("sk_stride_batch", _i64), ("sk_stride_draft", _i64), ("sk_stride_head", _i64),
+        ("suffix_value", _vp), ("sv_stride_batch", _i64), ("sv_stride_draft", _i64), ("sv_stride_head", _i64),
+        ("ancestor_mask", _vp), ("mask_stride_row", _i64), ("mask_stride_col", _i64),
+        ("prefix_output", _vp), ("po_stride_batch", _i64), ("po_stride_draft", _i64), ("po_stride_head", _i64),
+        ("prefix_dtype", _i32),
+        ("prefix_lse", _vp), ("pl_stride_batch", _i64), ("pl_stride_draft", _i64), ("pl_stride_head", _i64),
+        ("output", _vp), ("o_stride_batch", _i64), ("o_stride_draft", _i64), ("o_stride_head", _i64),
+        ("softmax_scale", _f32),
+        ("batch", _i32), ("draft_length", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
     ]
 
 
@@ -134,6 +154,11 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     lib.l20_pd_rope_and_cache.restype = _i32
     lib.l20_pd_kv_fp8_scales.argtypes = [kv_p, _vp, _vp, _i32, _vp]
     lib.l20_pd_kv_fp8_scales.restype = _i32
+    ts_p = ctypes.POINTER(L20PdTreeSuffixArgs)
+    lib.l20_pd_tree_suffix_check.argtypes = [ts_p]
+    lib.l20_pd_tree_suffix_check.restype = _i32
+    lib.l20_pd_tree_suffix_merge.argtypes = [ts_p, _vp]
+    lib.l20_pd_tree_suffix_merge.restype = _i32
     if path is None:
         _lib = lib
     return lib
@@ -274,4 +299,44 @@ def set_spin_limit(polls: int, lib: Optional[ctypes.CDLL] = None) -> None:
 def check(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> None:
     lib = lib or load()
     if lib.l20_pd_fp8_e4m3_check(ctypes.byref(args)) != L20_PD_OK:
+        raise RuntimeError(last_error(lib))
+
+
+def tree_suffix_args_from_tensors(query, suffix_key, suffix_value, ancestor_mask, prefix_output, prefix_lse,
+                                  output, softmax_scale: float) -> L20PdTreeSuffixArgs:
+    """Fill ``l20_pd_tree_suffix_args``: query/prefix_output/output [B, S, Hq, D],
+    suffix_key/value [B, S, Hkv, D], ancestor_mask bool [S, S], prefix_lse fp32
+    [B, S, Hq].  Keeps references to the tensors on the struct."""
+    a = L20PdTreeSuffixArgs()
+    a._tensors = (query, suffix_key, suffix_value, ancestor_mask, prefix_output, prefix_lse, output)
+    for name, t in (("query", query), ("suffix_key", suffix_key), ("suffix_value", suffix_value),
+                    ("prefix_output", prefix_output), ("output", output)):
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name}: head_dim must be the contiguous dimension")
+    a.query = query.data_ptr()
+    a.q_stride_batch, a.q_stride_draft, a.q_stride_head = query.stride()[:3]
+    a.query_dtype = _dtype_code(query)
+    a.suffix_key = suffix_key.data_ptr()
+    a.sk_stride_batch, a.sk_stride_draft, a.sk_stride_head = suffix_key.stride()[:3]
+    a.suffix_value = suffix_value.data_ptr()
+    a.sv_stride_batch, a.sv_stride_draft, a.sv_stride_head = suffix_value.stride()[:3]
+    a.ancestor_mask = ancestor_mask.data_ptr()
+    a.mask_stride_row, a.mask_stride_col = ancestor_mask.stride()
+    a.prefix_output = prefix_output.data_ptr()
+    a.po_stride_batch, a.po_stride_draft, a.po_stride_head = prefix_output.stride()[:3]
+    a.prefix_dtype = _dtype_code(prefix_output)
+    a.prefix_lse = prefix_lse.data_ptr()
+    a.pl_stride_batch, a.pl_stride_draft, a.pl_stride_head = prefix_lse.stride()
+    a.output = output.data_ptr()
+    a.o_stride_batch, a.o_stride_draft, a.o_stride_head = output.stride()[:3]
+    a.softmax_scale = float(softmax_scale)
+    a.batch, a.draft_length, a.num_q_heads, a.head_dim = query.shape
+    a.num_kv_heads = suffix_key.shape[2]
+    return a
+
+
+def tree_suffix_merge(args: L20PdTreeSuffixArgs, stream: int = 0, lib: Optional[ctypes.CDLL] = None) -> None:
+    """Call ``l20_pd_tree_suffix_merge``; raise RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    if lib.l20_pd_tree_suffix_merge(ctypes.byref(args), ctypes.c_void_p(stream)) != L20_PD_OK:
         raise RuntimeError(last_error(lib))

@@ -22,9 +22,11 @@ Two entry points:
   -- the reference's signatures, with the drafts' K/V in separate contiguous
   ``[B, S, Hkv, D]`` tensors next to a paged prefix of ``cached_length``
   tokens.  The prefix pass (the HBM-bound part) runs on the HIP kernel with
-  every draft key visible and returns its LSE; the S x S suffix attention and
-  the LSE merge are small fp32 torch ops.  Rows beyond the kernel's 32-column
-  tile are packed as extra batch entries that share the sequence's pages.
+  every draft row a query column and returns its LSE; ``l20_pd_tree_suffix_merge``
+  (one more launch) attends each row over its visible drafts and merges the
+  two in fp32.  Rows beyond the kernel's 32-column tile are packed as extra
+  batch entries that share the sequence's pages.  A ``TreeAttentionWorkspace``
+  keeps every buffer between calls, so warmed calls allocate nothing.
 
 The caches are fp8 e4m3fn (with ``k_scale``/``v_scale``) or the query's 16-bit
 dtype; head_dim 64 or 128; 16-token pages.
@@ -78,17 +80,21 @@ def _scale_args(scale: Scale) -> Tuple[float, Optional[torch.Tensor]]:
 def _paged_call(rows_q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                 block_table: torch.Tensor, seq_lens: torch.Tensor, q_len: int, max_seq_len: int,
                 split_size: Optional[int], softmax_scale: float, k_scale: Scale, v_scale: Scale,
-                tree_words: torch.Tensor, output: torch.Tensor, lse: Optional[torch.Tensor]) -> torch.Tensor:
-    """One launch of the split-KV kernel in tree mode over ``rows_q`` [B*q_len, Hq, D]."""
+                tree_words: torch.Tensor, output: torch.Tensor, lse: Optional[torch.Tensor],
+                partials=None) -> torch.Tensor:
+    """One launch of the split-KV kernel in tree mode over ``rows_q`` [B*q_len, Hq, D];
+    ``partials`` (output, max, sum) is the split workspace (allocated when None)."""
     batch = rows_q.shape[0] // q_len
     num_q_heads, head_dim = rows_q.shape[1], rows_q.shape[2]
     if split_size is None:
         split_size = default_split_size(batch, key_cache.shape[2], max_seq_len, rows_q.device)
-    n_s = max(1, math.ceil(max_seq_len / split_size)) if max_seq_len > 0 else 1
-    shape = (rows_q.shape[0], num_q_heads, n_s)
-    po = torch.empty((*shape, head_dim), device=rows_q.device, dtype=torch.float32)
-    pm = torch.empty(shape, device=rows_q.device, dtype=torch.float32)
-    ps = torch.empty(shape, device=rows_q.device, dtype=torch.float32)
+    if partials is None:
+        n_s = max(1, math.ceil(max_seq_len / split_size)) if max_seq_len > 0 else 1
+        shape = (rows_q.shape[0], num_q_heads, n_s)
+        partials = (torch.empty((*shape, head_dim), device=rows_q.device, dtype=torch.float32),
+                    torch.empty(shape, device=rows_q.device, dtype=torch.float32),
+                    torch.empty(shape, device=rows_q.device, dtype=torch.float32))
+    po, pm, ps = partials
     if key_cache.dtype == torch.float8_e4m3fn:
         ks, ks_ph = _scale_args(k_scale)
         vs, vs_ph = _scale_args(v_scale)
@@ -165,33 +171,55 @@ def paged_tree_verify_attention(
     return out.view_as(query) if output is None else output
 
 
-def allocate_tree_attention_workspace(query: torch.Tensor):
-    """Prefix and suffix summaries of the split tree attention (the reference's
-    six-tensor layout, ``triton_tree_attention.py:761-776``): output fp32
-    [B, S, Hq, D], max and sum fp32 [B, S, Hq], for the prefix then the suffix.
-    Here the max slot holds the natural-log LSE of the part and the sum slot 1."""
+class TreeAttentionWorkspace(tuple):
+    """The reference's six summary tensors (``triton_tree_attention.py:761-776``:
+    output fp32 [B, S, Hq, D], max and sum fp32 [B, S, Hq], for the prefix then
+    the suffix), which unpack as a tuple, plus the buffers the MI355X path
+    needs: created by the first call that uses them and reused by every later
+    call of the same shapes, so a warmed workspace makes
+    ``hybrid_tree_attention_paged_prefix`` allocate nothing (and lets it be
+    captured in a HIP graph)."""
+
+    def __new__(cls, tensors):
+        obj = super().__new__(cls, tensors)
+        obj._buffers = {}
+        return obj
+
+    def buffer(self, name: str, shape, dtype: torch.dtype, device) -> torch.Tensor:
+        shape = tuple(int(x) for x in shape)
+        t = self._buffers.get(name)
+        if t is None or tuple(t.shape) != shape or t.dtype != dtype or t.device != torch.device(device):
+            t = torch.empty(shape, dtype=dtype, device=device)
+            self._buffers[name] = t
+        return t
+
+    def constant(self, name: str, make, shape) -> torch.Tensor:
+        """A tensor made once by ``make()`` and kept while its shape stays ``shape``."""
+        t = self._buffers.get(name)
+        if t is None or tuple(t.shape) != tuple(shape):
+            t = make()
+            self._buffers[name] = t
+        return t
+
+
+def allocate_tree_attention_workspace(query: torch.Tensor) -> TreeAttentionWorkspace:
+    """Workspace of the split tree attention (the reference's six-tensor layout,
+    ``triton_tree_attention.py:761-776``); see ``TreeAttentionWorkspace``."""
     if query.ndim != 4:
         raise ValueError("expected query=[B,S,Hq,D]")
     batch, draft_length, num_q_heads, head_dim = query.shape
     summary = (batch, draft_length, num_q_heads)
     f32 = dict(device=query.device, dtype=torch.float32)
-    return (torch.empty((*summary, head_dim), **f32), torch.empty(summary, **f32), torch.empty(summary, **f32),
-            torch.empty((*summary, head_dim), **f32), torch.empty(summary, **f32), torch.empty(summary, **f32))
+    return TreeAttentionWorkspace(
+        (torch.empty((*summary, head_dim), **f32), torch.empty(summary, **f32), torch.empty(summary, **f32),
+         torch.empty((*summary, head_dim), **f32), torch.empty(summary, **f32), torch.empty(summary, **f32)))
 
 
-def _suffix_attention(query: torch.Tensor, suffix_key: torch.Tensor, suffix_value: torch.Tensor,
-                      visible: torch.Tensor, scale: float) -> Tuple[torch.Tensor, torch.Tensor]:
-    """fp32 attention of the S draft rows over the S draft keys: (out [B,S,Hq,D], lse [B,S,Hq])."""
-    group = query.shape[2] // suffix_key.shape[2]
-    q = query.float().permute(0, 2, 1, 3).contiguous()  # [B, Hq, S, D]
-    k = suffix_key.float().repeat_interleave(group, dim=2).permute(0, 2, 3, 1).contiguous()  # [B, Hq, D, S]
-    v = suffix_value.float().repeat_interleave(group, dim=2).permute(0, 2, 1, 3).contiguous()  # [B, Hq, S, D]
-    scores = torch.matmul(q, k) * scale
-    scores = scores.masked_fill(~visible, float("-inf"))
-    lse = torch.logsumexp(scores, dim=-1)  # [B, Hq, S]
-    probs = torch.exp(scores - torch.where(torch.isfinite(lse), lse, torch.zeros_like(lse))[..., None])
-    out = torch.matmul(probs, v)
-    return out.permute(0, 2, 1, 3), lse.permute(0, 2, 1)
+def _check_block_t(block_t: Optional[int]) -> None:
+    # The reference's Triton tile knob (triton_tree_attention.py:1071-1074); the
+    # HIP kernel's tiling is fixed, so it is only validated.
+    if block_t is not None and block_t not in (32, 64, 128):
+        raise ValueError("block_t must be one of 32, 64, or 128")
 
 
 def hybrid_tree_attention_paged_prefix(
@@ -205,72 +233,111 @@ def hybrid_tree_attention_paged_prefix(
     cached_length: int,
     *,
     workspace=None,
+    block_t: Optional[int] = None,
+    contiguous_pages: bool = False,
+    page_base: Optional[torch.Tensor] = None,
     k_scale: Scale = 1.0,
     v_scale: Scale = 1.0,
     split_size: Optional[int] = None,
     softmax_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Tree attention over a paged prefix of ``cached_length`` tokens plus a contiguous
     draft suffix (``triton_tree_attention.py:1040-1197``).
 
     query [B, S, Hq, D]; key/value_cache [pages, 16, Hkv, D]; suffix_key/value
-    [B, S, Hkv, D] (query dtype); block_table [B, pages] covering cached_length;
-    ancestor_mask [S, S] bool.  Returns [B, S, Hq, D] in the query dtype.
+    [B, S, Hkv, D] (query dtype); block_table [B, pages] covering cached_length
+    (with ``contiguous_pages`` the pages of sequence b are ``page_base[b] + t // 16``
+    instead, as in the reference); ancestor_mask [S, S] bool on the query's device.
+    Returns [B, S, Hq, D] in the query dtype (``output`` when given).
+
+    Two launches of the HIP library: the prefix pass (the split-KV kernel with every
+    draft row a query column, LSE out) and ``l20_pd_tree_suffix_merge`` (suffix
+    attention and LSE merge in fp32).  With a ``TreeAttentionWorkspace`` from
+    ``allocate_tree_attention_workspace`` and an ``output`` tensor, a call after the
+    first of the same shapes allocates nothing; float (or [Hkv] tensor) scales keep
+    it free of host synchronisation.
     """
     _check_common(query, key_cache, value_cache)
     if query.ndim != 4:
         raise ValueError("expected query=[B,S,Hq,D]")
     if suffix_key.ndim != 4 or suffix_value.shape != suffix_key.shape:
         raise ValueError("expected suffix key/value=[B,S,Hkv,D]")
+    if block_table.ndim != 2:
+        raise ValueError("expected block_table=[B,pages]")
     batch, draft, num_q_heads, head_dim = query.shape
     num_kv_heads = key_cache.shape[2]
     if suffix_key.shape != (batch, draft, num_kv_heads, head_dim):
         raise ValueError("suffix KV must match query batch/draft and cache kv heads")
-    if block_table.ndim != 2 or block_table.shape[0] != batch or block_table.shape[1] * 16 < cached_length:
+    if suffix_key.dtype != query.dtype or suffix_value.dtype != query.dtype:
+        raise ValueError("suffix key/value must have the query's dtype")
+    if block_table.shape[0] != batch or block_table.shape[1] * 16 < cached_length:
         raise ValueError("block_table does not cover cached_length")
     if ancestor_mask.shape != (draft, draft):
         raise ValueError("ancestor_mask must match draft_length")
     if draft < 1 or draft > MAX_DRAFT:
         raise ValueError("paged suffix path supports draft_length in [1, 64]")
+    _check_block_t(block_t)
+    if contiguous_pages:
+        if page_base is None:
+            raise ValueError("contiguous_pages=True requires page_base=[B]")
+        if page_base.ndim != 1 or page_base.shape[0] != batch:
+            raise ValueError("page_base must have shape [B]")
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
-    if workspace is None:
-        workspace = allocate_tree_attention_workspace(query)
-    prefix_out, prefix_lse, prefix_one, suffix_out, suffix_lse, suffix_one = workspace
+    ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
+    dev = query.device
+    if output is None:
+        output = torch.empty_like(query)
+    elif output.shape != query.shape or output.dtype != query.dtype:
+        raise ValueError("output must be shaped like the query, in its dtype")
 
-    # Prefix: every draft row sees all cached_length keys.  Rows are packed c at a
-    # time (c x group <= 32 query columns) as extra batch entries on the same pages.
+    # Prefix pass: every draft row sees all cached_length keys.  Rows are packed c at
+    # a time (c x group <= 32 query columns) as extra batch entries on the same pages.
     group = num_q_heads // num_kv_heads
     cols = max(1, min(draft, MAX_COLUMNS // group, 32))
     chunks = math.ceil(draft / cols)
     padded = chunks * cols
-    q = query
-    if padded != draft:
-        q = torch.zeros((batch, padded, num_q_heads, head_dim), dtype=query.dtype, device=query.device)
-        q[:, :draft] = query
-    rows_q = q.reshape(batch * chunks * cols, num_q_heads, head_dim)
-    table = block_table.repeat_interleave(chunks, dim=0) if chunks > 1 else block_table
-    lens = torch.full((batch * chunks,), int(cached_length), dtype=torch.int32, device=query.device)
-    all_visible = torch.full((cols,), -1 if cols == 32 else (1 << cols) - 1, dtype=torch.int32,
-                             device=query.device)
-    p_out = torch.empty((rows_q.shape[0], num_q_heads, head_dim), dtype=query.dtype, device=query.device)
-    p_lse = torch.empty((rows_q.shape[0], num_q_heads), dtype=torch.float32, device=query.device)
-    _paged_call(rows_q, key_cache, value_cache, table.contiguous(), lens, cols, int(cached_length), split_size,
-                scale, k_scale, v_scale, all_visible, p_out, p_lse)
-    prefix_out.copy_(p_out.view(batch, padded, num_q_heads, head_dim)[:, :draft])
-    prefix_lse.copy_(p_lse.view(batch, padded, num_q_heads)[:, :draft])
-    prefix_one.fill_(1.0)
+    entries = batch * chunks
+    if padded == draft and query.is_contiguous():
+        rows_q = query.view(entries * cols, num_q_heads, head_dim)
+    else:
+        qb = ws.buffer("query", (batch, padded, num_q_heads, head_dim), query.dtype, dev)
+        qb[:, :draft].copy_(query)
+        if padded != draft:
+            qb[:, draft:].zero_()
+        rows_q = qb.view(entries * cols, num_q_heads, head_dim)
+    pages = max(1, math.ceil(cached_length / 16))
+    if contiguous_pages:
+        ramp = ws.constant("ramp", lambda: torch.arange(pages, dtype=torch.int32, device=dev), (pages,))
+        table = ws.buffer("table", (entries, pages), torch.int32, dev)
+        torch.add(page_base.to(torch.int32)[:, None, None], ramp[None, None, :], out=table.view(batch, chunks, pages))
+    elif chunks > 1:
+        table = ws.buffer("table", (entries, block_table.shape[1]), torch.int32, dev)
+        table.view(batch, chunks, -1).copy_(block_table[:, None, :].expand(batch, chunks, block_table.shape[1]))
+    else:
+        table = block_table
+    lens = ws.buffer("lens", (entries,), torch.int32, dev)
+    lens.fill_(int(cached_length))
+    words = ws.buffer("words", (cols,), torch.int32, dev)
+    words.fill_(-1 if cols == 32 else (1 << cols) - 1)
+    if split_size is None:
+        split_size = default_split_size(entries, num_kv_heads, int(cached_length), dev)
+    n_s = max(1, math.ceil(cached_length / split_size)) if cached_length > 0 else 1
+    n_rows = entries * cols
+    partials = (ws.buffer("partial_output", (n_rows, num_q_heads, n_s, head_dim), torch.float32, dev),
+                ws.buffer("partial_max", (n_rows, num_q_heads, n_s), torch.float32, dev),
+                ws.buffer("partial_sum", (n_rows, num_q_heads, n_s), torch.float32, dev))
+    p_out = ws.buffer("prefix_output", (n_rows, num_q_heads, head_dim), query.dtype, dev)
+    p_lse = ws.buffer("prefix_lse", (n_rows, num_q_heads), torch.float32, dev)
+    _paged_call(rows_q, key_cache, value_cache, table, lens, cols, int(cached_length), split_size,
+                scale, k_scale, v_scale, words, p_out, p_lse, partials=partials)
 
-    visible = ancestor_mask.to(device=query.device, dtype=torch.bool)[None, None]
-    s_out, s_lse = _suffix_attention(query, suffix_key, suffix_value, visible, scale)
-    suffix_out.copy_(s_out)
-    suffix_lse.copy_(s_lse)
-    suffix_one.fill_(1.0)
-
-    m = torch.maximum(prefix_lse, suffix_lse)
-    w_p = torch.exp(prefix_lse - m)
-    w_s = torch.exp(suffix_lse - m)
-    out = (w_p[..., None] * prefix_out + w_s[..., None] * suffix_out) / (w_p + w_s)[..., None]
-    return out.to(query.dtype)
+    # Suffix attention and LSE merge in one launch.
+    torch.ops.l20_stack.tree_suffix_merge(
+        query, suffix_key, suffix_value, ancestor_mask,
+        p_out.view(batch, padded, num_q_heads, head_dim)[:, :draft],
+        p_lse.view(batch, padded, num_q_heads)[:, :draft], output, scale)
+    return output
 
 
 def causal_verifier_attention_paged(
@@ -282,16 +349,24 @@ def causal_verifier_attention_paged(
     block_table: torch.Tensor,
     cached_length: int,
     *,
+    block_t: Optional[int] = None,
+    workspace=None,
     k_scale: Scale = 1.0,
     v_scale: Scale = 1.0,
     split_size: Optional[int] = None,
     softmax_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """The chain special case (``triton_tree_attention.py:966-1037``): draft row i sees
-    the cached prefix and drafts 0..i."""
+    the cached prefix and drafts 0..i.  The chain mask is kept in the workspace."""
     if query.ndim != 4:
         raise ValueError("expected query=[B,S,Hq,D]")
+    draft = query.shape[1]
+    if draft < 1 or draft > MAX_DRAFT:
+        raise ValueError("causal verifier path supports draft_length in [1, 64]")
+    ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
+    chain = ws.constant("chain_mask", lambda: make_chain_tree_mask(draft, device=query.device), (draft, draft))
     return hybrid_tree_attention_paged_prefix(
-        query, key_cache, value_cache, suffix_key, suffix_value, block_table,
-        make_chain_tree_mask(query.shape[1], device=query.device), cached_length,
-        k_scale=k_scale, v_scale=v_scale, split_size=split_size, softmax_scale=softmax_scale)
+        query, key_cache, value_cache, suffix_key, suffix_value, block_table, chain, cached_length,
+        workspace=ws, block_t=block_t, k_scale=k_scale, v_scale=v_scale, split_size=split_size,
+        softmax_scale=softmax_scale, output=output)

@@ -40,7 +40,7 @@ def test_library_exports_every_header_symbol():
     assert sorted(cabi.EXPORTED) == declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.l20_pd_abi_version() == cabi.ABI_VERSION == 3
+    assert lib.l20_pd_abi_version() == cabi.ABI_VERSION == 4
 
 
 def test_num_splits_and_default_split_size():
@@ -329,3 +329,30 @@ def test_check_16bit_caches_and_csr():
     a.v_stride_head = 132
     with pytest.raises(RuntimeError, match="V cache pointer and strides must be aligned"):
         cabi.check(a)
+
+
+def test_tree_suffix_check_validates_without_a_gpu():
+    """l20_pd_tree_suffix_check (include/l20_tree_verify.h): the reference's limits
+    (draft_length 1..64, integral GQA ratio) plus head_dim 64/128 and the dtypes."""
+    lib = cabi.load()
+
+    def args(**kw):
+        a = cabi.L20PdTreeSuffixArgs()
+        for name in ("query", "suffix_key", "suffix_value", "ancestor_mask", "prefix_output", "prefix_lse", "output"):
+            setattr(a, name, 4096)  # never dereferenced by the check
+        a.query_dtype = a.prefix_dtype = cabi.L20_PD_BF16
+        a.softmax_scale = 0.125
+        a.batch, a.draft_length, a.num_q_heads, a.num_kv_heads, a.head_dim = 2, 8, 28, 4, 128
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return ctypes.byref(a)
+
+    assert lib.l20_pd_tree_suffix_check(args()) == cabi.L20_PD_OK
+    assert lib.l20_pd_tree_suffix_check(args(prefix_dtype=cabi.L20_PD_FP32, head_dim=64)) == cabi.L20_PD_OK
+    for kw, msg in [(dict(draft_length=65), "draft_length"), (dict(draft_length=0), "draft_length"),
+                    (dict(head_dim=96), "head_dim"), (dict(num_kv_heads=3), "GQA"),
+                    (dict(query_dtype=cabi.L20_PD_FP32), "bf16 or fp16"),
+                    (dict(prefix_dtype=cabi.L20_PD_FP16), "prefix output"),
+                    (dict(output=0), "null"), (dict(softmax_scale=0.0), "softmax_scale")]:
+        assert lib.l20_pd_tree_suffix_check(args(**kw)) == cabi.L20_PD_EINVAL, kw
+        assert msg in cabi.last_error(lib), (kw, cabi.last_error(lib))

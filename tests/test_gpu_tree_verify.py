@@ -249,3 +249,134 @@ def test_paged_tree_verify_rejects_wide_tiles():
         tv.paged_tree_verify_attention(q, kc, kc, torch.zeros(1, 4, dtype=torch.int32, device="cuda"),
                                        torch.full((1,), 40, dtype=torch.int32, device="cuda"),
                                        tv.make_chain_tree_mask(8, device="cuda"))
+
+
+# ------------------------------------------------------------------ the fused suffix + merge kernel
+@pytest.mark.parametrize("d,qdt,prefix_f32", [(128, torch.bfloat16, False), (64, torch.float16, True),
+                                             (128, torch.float16, True)])
+def test_tree_suffix_merge_c_abi_against_closed_form(d, qdt, prefix_f32):
+    """out = (e^lse o_p + sum_j e^s_j v_j) / (e^lse + sum_j e^s_j) over the visible
+    drafts, in float64; a row with an empty prefix (lse = -inf) and no visible
+    draft is zero; 40 drafts exercise several key batches."""
+    import l20_pd_cabi as cabi
+
+    b, s, hq, hkv = 3, 40, 8, 2
+    g = torch.Generator().manual_seed(d + s)
+    q = torch.randn(b, s, hq, d, generator=g).to(qdt)
+    sk = torch.randn(b, s, hkv, d, generator=g).to(qdt)
+    sv = torch.randn(b, s, hkv, d, generator=g).to(qdt)
+    mask = torch.from_numpy(random_tree(s, np.random.default_rng(3)))
+    mask[5] = False                               # row 5 sees no draft
+    po = torch.randn(b, s, hq, d, generator=g).to(torch.float32 if prefix_f32 else qdt)
+    pl = torch.randn(b, s, hq, generator=g) * 3
+    pl[1, 5, :] = float("-inf")                   # ... and, in sequence 1, no prefix either
+    pl[2, :, 3] = float("-inf")                   # head 3 of sequence 2: suffix only
+    scale = 0.3
+    out = torch.empty(b, s, hq, d, dtype=qdt, device="cuda")
+    t = [x.cuda() for x in (q, sk, sv, mask, po, pl)]
+    args = cabi.tree_suffix_args_from_tensors(*t, out, scale)
+    cabi.tree_suffix_merge(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+
+    qf, kf, vf = q.double().numpy(), sk.double().numpy(), sv.double().numpy()
+    pof, plf, m = po.double().numpy(), pl.double().numpy(), mask.numpy()
+    grp = hq // hkv
+    exp = np.zeros((b, s, hq, d))
+    for bi in range(b):
+        for i in range(s):
+            for h in range(hq):
+                sc = kf[bi, :, h // grp] @ qf[bi, i, h] * scale
+                w = np.where(m[i], np.exp(sc), 0.0)
+                wp = np.exp(plf[bi, i, h])
+                num = w @ vf[bi, :, h // grp] + (wp * pof[bi, i, h] if wp > 0 else 0.0)
+                den = w.sum() + wp
+                exp[bi, i, h] = num / den if den > 0 else 0.0
+    got = out.double().cpu().numpy()
+    assert np.array_equal(got[1, 5], np.zeros((hq, d)))
+    # the 16-bit output's own rounding bounds the error (half an ulp: 2^-9 relative for
+    # bf16, 2^-12 for fp16; twice that here), plus 1e-3 for fp32 arithmetic
+    rel = 2.0 ** -8 if qdt == torch.bfloat16 else 2.0 ** -11
+    assert np.all(np.abs(got - exp) <= rel * np.abs(exp) + 1e-3)
+
+
+def _hybrid_inputs(batch, hq, hkv, d, cached, draft, seed, kv=torch.bfloat16):
+    kc, vc, ks, vs, table, pk, pv = _paged_prefix(batch, hkv, d, cached, kv, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    qdt = torch.bfloat16 if kv in ("fp8", torch.bfloat16) else torch.float16
+    query = torch.randn(batch, draft, hq, d, generator=g).to(qdt).cuda()
+    sk = torch.randn(batch, draft, hkv, d, generator=g).to(qdt).cuda()
+    sv = torch.randn(batch, draft, hkv, d, generator=g).to(qdt).cuda()
+    mask = torch.from_numpy(random_tree(draft, np.random.default_rng(seed))).cuda()
+    return dict(query=query, kc=kc, vc=vc, ks=ks, vs=vs, table=table, sk=sk, sv=sv, mask=mask, pk=pk, pv=pv)
+
+
+@pytest.mark.parametrize("draft,hq,hkv", [(8, 28, 4), (5, 8, 2)])  # two packed chunks; one padded chunk
+def test_hybrid_warmed_workspace_allocates_nothing_and_replays_in_a_graph(draft, hq, hkv):
+    import l20_tree_verify as tv
+
+    x = _hybrid_inputs(2, hq, hkv, 128, 1500, draft, seed=draft, kv="fp8")
+    ws = tv.allocate_tree_attention_workspace(x["query"])
+    out = torch.empty_like(x["query"])
+
+    def call():
+        return tv.hybrid_tree_attention_paged_prefix(
+            x["query"], x["kc"], x["vc"], x["sk"], x["sv"], x["table"], x["mask"], 1500,
+            workspace=ws, k_scale=x["ks"], v_scale=x["vs"], output=out)
+
+    call()
+    torch.cuda.synchronize()
+    first = out.clone()
+    exp = _dense_oracle(x["query"].float().cpu().numpy(), x["pk"], x["pv"], x["sk"].float().cpu().numpy(),
+                        x["sv"].float().cpu().numpy(), x["mask"].cpu().numpy(), 128 ** -0.5)
+    assert np.abs(first.float().cpu().numpy() - exp).max() <= H.OUT_ATOL
+    before = torch.cuda.memory_stats()["allocation.all.allocated"]
+    call()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_stats()["allocation.all.allocated"] == before, "a warmed call allocated"
+    assert torch.equal(out, first)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            call()
+    torch.cuda.synchronize()
+    q0 = x["query"].clone()
+    for r in range(3):
+        # new draft queries in place, then a replay against an eager call on them
+        x["query"].copy_(q0 * (1.0 + 0.25 * r))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        call()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, out), r
+
+
+def test_hybrid_contiguous_pages_equal_block_table():
+    import l20_tree_verify as tv
+
+    batch, hq, hkv, d, cached, draft = 3, 16, 4, 128, 700, 6
+    pages = (cached + 15) // 16
+    g = torch.Generator().manual_seed(8)
+    base = torch.tensor([5, 5 + pages + 2, 5 + 2 * pages + 9], dtype=torch.int32)
+    pool = int(base.max()) + pages + 1
+    kc = torch.randn(pool, 16, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    vc = torch.randn(pool, 16, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    table = (base[:, None] + torch.arange(pages, dtype=torch.int32)[None, :]).cuda()
+    query = torch.randn(batch, draft, hq, d, generator=g).to(torch.bfloat16).cuda()
+    sk = torch.randn(batch, draft, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    sv = torch.randn(batch, draft, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    mask = torch.from_numpy(random_tree(draft, np.random.default_rng(1))).cuda()
+    a = tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached)
+    junk = torch.full_like(table, -1)  # ignored with contiguous pages
+    b = tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, junk, mask, cached,
+                                              contiguous_pages=True, page_base=base.cuda(), block_t=128)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError, match="block_t"):
+        tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, block_t=48)
+    with pytest.raises(ValueError, match="page_base"):
+        tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, contiguous_pages=True)
