@@ -182,6 +182,11 @@ def _register_fake() -> None:
     ):
         return output
 
+    @torch.library.register_fake("l20_stack::tree_suffix_merge")
+    def _tree_suffix_merge_fake(query, suffix_key, suffix_value, ancestor_mask, prefix_output, prefix_lse, output,
+                                softmax_scale):
+        return None
+
 
 load_library()
 _register_fake()

@@ -356,3 +356,16 @@ def test_tree_suffix_check_validates_without_a_gpu():
                     (dict(output=0), "null"), (dict(softmax_scale=0.0), "softmax_scale")]:
         assert lib.l20_pd_tree_suffix_check(args(**kw)) == cabi.L20_PD_EINVAL, kw
         assert msg in cabi.last_error(lib), (kw, cabi.last_error(lib))
+
+
+def test_tree_suffix_merge_op_schema_and_fake():
+    import l20_paged_decode  # noqa: F401
+
+    schema = str(torch.ops.l20_stack.tree_suffix_merge.default._schema)
+    assert "Tensor(a!) output" in schema and schema.endswith("-> ()")
+    m = dict(device="meta")
+    q = torch.empty(2, 4, 8, 128, dtype=torch.bfloat16, **m)
+    kv = torch.empty(2, 4, 2, 128, dtype=torch.bfloat16, **m)
+    mask = torch.empty(4, 4, dtype=torch.bool, **m)
+    lse = torch.empty(2, 4, 8, dtype=torch.float32, **m)
+    assert torch.ops.l20_stack.tree_suffix_merge(q, kv, kv, mask, q, lse, torch.empty_like(q), 0.1) is None
