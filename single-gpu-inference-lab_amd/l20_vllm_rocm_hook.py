@@ -18,7 +18,10 @@ reference's:
 
 * ``VLLM_ENABLE_L20_FP8_PAGED_DECODE=1`` turns the path on (off by default);
 * the device is an MI355X (gfx950; the reference required SM89), no graph is
-  being captured, the KV cache is fp8 (``float8_e4m3fn`` views) in 16-token
+  being captured, the KV cache is fp8 (``kv_cache_dtype`` "fp8"/"fp8_e4m3" for
+  OCP e4m3fn bytes or "fp8_e5m2" for e5m2 bytes -- the reference's hook takes every
+  quantized cache, and vLLM's backend views both as its platform fp8 type, so the
+  op gets the bytes re-viewed in the setting's format) in 16-token
   pages with head_size 64/128, the batch is pure decode (``max_query_len == 1``)
   and the layer uses none of ALiBi, sliding windows, logit soft-capping,
   attention sinks or a fused output quantisation (``output_scale`` given, or an
@@ -60,6 +63,23 @@ def _unsupported_features(impl: Any) -> bool:
     )
 
 
+_FP8_BYTES = (torch.float8_e4m3fn, torch.float8_e5m2, torch.uint8)
+
+
+def cache_format(impl: Any) -> Optional[torch.dtype]:
+    """The torch dtype that the cache bytes hold, from vLLM's ``kv_cache_dtype``
+    ("fp8" and "fp8_e4m3": OCP e4m3fn on gfx950; "fp8_e5m2": e5m2), or None for a
+    cache this path does not read.  vLLM's Triton backend views every fp8 cache
+    as the platform's fp8 type, so the format comes from the setting, not from
+    the tensor's dtype."""
+    kind = str(getattr(impl, "kv_cache_dtype", ""))
+    if kind in ("fp8", "fp8_e4m3"):
+        return torch.float8_e4m3fn
+    if kind == "fp8_e5m2":
+        return torch.float8_e5m2
+    return None
+
+
 def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Tensor,
                 value_cache: torch.Tensor, attn_metadata: Any, num_actual_tokens: int,
                 output: Optional[torch.Tensor] = None, output_scale: Any = None) -> bool:
@@ -73,7 +93,7 @@ def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Ten
 
     if os.getenv(ENABLE_ENV, "0") != "1":
         return False
-    if not str(getattr(impl, "kv_cache_dtype", "")).startswith("fp8"):
+    if cache_format(impl) is None:
         return False
     if getattr(attn_metadata, "max_query_len", None) != 1:
         return False
@@ -85,7 +105,7 @@ def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Ten
                                or output.shape[0] < num_actual_tokens
                                or output[0].numel() != query[0].numel()):
         return False
-    if key_cache.dtype != torch.float8_e4m3fn or value_cache.dtype != torch.float8_e4m3fn:
+    if key_cache.dtype not in _FP8_BYTES or value_cache.dtype not in _FP8_BYTES:
         return False
     if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
         return False
@@ -127,8 +147,10 @@ def l20_fp8_paged_decode_or_none(impl: Any, layer: Any, query: torch.Tensor, key
     if getattr(impl, "_l20_fp8_workspace_shape", None) != shape:
         impl._l20_fp8_workspace = allocate_l20_paged_split_kv_workspace(q, max_seq_len, split_size=SPLIT_SIZE)
         impl._l20_fp8_workspace_shape = shape
+    fmt = cache_format(impl)
     l20_paged_split_kv_attention_fp8(
-        q, key_cache, value_cache, attn_metadata.block_table[:batch], attn_metadata.seq_lens[:batch],
+        q, key_cache.view(fmt), value_cache.view(fmt), attn_metadata.block_table[:batch],
+        attn_metadata.seq_lens[:batch],
         k_scale=float(layer._k_scale_float), v_scale=float(layer._v_scale_float),
         max_seq_len=max_seq_len, split_size=SPLIT_SIZE, output=output[:batch].view_as(q),
         workspace=impl._l20_fp8_workspace, softmax_scale=float(impl.scale),

@@ -72,3 +72,32 @@ def test_patched_forward_runs_the_op_and_traces(tmp_path, monkeypatch):
     impl.forward(layer, q, None, None, kv, meta, output=torch.zeros(8, 16, 128, device="cuda").to(torch.float8_e4m3fn))
     assert len(mod.CALLS) == 4
     assert len(trace.read_text().splitlines()) == 2
+
+
+def test_patched_forward_reads_e5m2_caches_in_their_format(tmp_path, monkeypatch):
+    """kv_cache_dtype "fp8_e5m2": vLLM's backend views the cache as its platform
+    fp8 type (e4m3fn here); the hook re-views the bytes as e5m2, so the result
+    is the e5m2 oracle's, not that of the same bytes read as e4m3fn."""
+    import install_l20_fp8_paged_decode_rocm as inst
+    import l20_vllm_rocm_hook as hook
+
+    shutil.copytree(FIXTURE, tmp_path / "src")
+    inst.main(["--vllm-source-dir", str(tmp_path / "src")])
+    monkeypatch.syspath_prepend(str(tmp_path / "src"))
+    for name in [m for m in sys.modules if m == "vllm" or m.startswith("vllm.")]:
+        monkeypatch.delitem(sys.modules, name)
+    mod = importlib.import_module("vllm.v1.attention.backends.triton_attn")
+    monkeypatch.setenv(hook.ENABLE_ENV, "1")
+    monkeypatch.setenv(hook.FORCE_ENV, "1")
+    inp = H.make_synthetic(4, 16, 2, 128, [700, 31, 1500, 64], seed=13, fp8="e5m2")
+    kv = torch.stack([inp["key_cache"].view(torch.uint8), inp["value_cache"].view(torch.uint8)])
+    impl = mod.TritonAttentionImpl(16, 128, inp["softmax_scale"], 2, kv_cache_dtype="fp8_e5m2")
+    layer = types.SimpleNamespace(_k_scale_float=inp["k_scale"], _v_scale_float=inp["v_scale"])
+    meta = types.SimpleNamespace(num_actual_tokens=4, query_start_loc=None, seq_lens=inp["seq_lens"],
+                                 max_query_len=1, max_seq_len=inp["max_seq_len"], block_table=inp["block_table"])
+    out = torch.zeros(4, 16, 128, dtype=torch.bfloat16, device="cuda")
+    impl.forward(layer, inp["query"], None, None, kv, meta, output=out)
+    torch.cuda.synchronize()
+    assert mod.CALLS == []
+    exp_out, _ = H.run_oracle(inp)  # e5m2 format (the cache tensors' dtype)
+    H.compare(out, None, exp_out, None, check_lse=False)

@@ -99,7 +99,13 @@ def test_gate_rejects_each_unsupported_case(monkeypatch):
         impl2 = types.SimpleNamespace(**vars(impl))
         setattr(impl2, attr, value)
         assert not hook.decode_gate(impl2, layer, q, kc, vc, meta, n), attr
-    assert not hook.decode_gate(impl, layer, q, kc.view(torch.uint8), vc, meta, n)  # not an e4m3fn view
+    assert not hook.decode_gate(impl, layer, q, kc.view(torch.int8), vc, meta, n)  # not a byte view of fp8 codes
+    assert not hook.decode_gate(*_fake_call(kv_dtype="fp8_e4m3fnuz"))  # a format the op does not read
+    # e5m2 caches take the path; vLLM's backend hands them over viewed as its platform type
+    assert hook.decode_gate(*_fake_call(kv_dtype="fp8_e5m2"))
+    assert hook.cache_format(types.SimpleNamespace(kv_cache_dtype="fp8_e5m2")) == torch.float8_e5m2
+    for kind in ("fp8", "fp8_e4m3"):
+        assert hook.cache_format(types.SimpleNamespace(kv_cache_dtype=kind)) == torch.float8_e4m3fn
     monkeypatch.setattr(l20_paged_split_kv, "is_mi355x", lambda device=None: False)
     assert not hook.decode_gate(impl, layer, q, kc, vc, meta, n)  # not gfx950
     monkeypatch.setattr(l20_paged_split_kv, "is_mi355x", lambda device=None: True)
