@@ -315,7 +315,7 @@ __device__ unsigned int g_pd_spin_limit = kSpinLimit;
 // MFMA tile (G x q_len query rows, padded to 16 * NQT), j = lane / 16.
 // Blocks hold 32 fp8 tokens (two 16-token pages: tiles 2*blk, 2*blk + 1 of
 // the unit's page-id window) or 16 tokens of a 16-bit cache (tile blk).
-template <typename QT, int KT, int D, int NQT, bool TREE>
+template <typename QT, int KT, int D, int NQT, bool TREE, bool KLINES>
 struct KvUnit {
   typedef typename MfmaTypes<QT>::vec8 qvec8;
   typedef typename KvBlock<KT, D>::type Block;
@@ -335,6 +335,20 @@ struct KvUnit {
   static constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
   static constexpr int NT = D / 16;   // 16-row d tiles of the PV product
   static constexpr int DPL = D / 4;   // contiguous output dims per lane
+  // KLINES (fp8 K at head_dim 128, one block in flight): K arrives in whole
+  // 128-byte lines (lane l: token 8c + l/8 of page T, bytes 16 (l % 8)) and
+  // goes through the wave's own LDS rows into the MFMA layout (lane (n16, j):
+  // token n16, bytes 16 j + 64 c).  Loading the MFMA layout straight from
+  // memory takes half of 16 lines per instruction; in load-only kernels over
+  // the config-3 pages and schedule that streamed at 4.7 TB/s against 5.6 for
+  // whole lines.  In the full kernels the pass gains 1.6 us at config 4 (85.4
+  // vs 87.1 us, same box) and nothing at config 5, both one block in flight,
+  // but costs 1.1 us in the two-block kernel of config 3 (10 more VGPRs), which
+  // keeps the direct loads.  Rows are padded to 144 bytes so that the 16 rows
+  // of a read fall in distinct banks.
+  static constexpr bool kKLines = KLINES;
+  static constexpr int kKxRow = 144;                  // LDS bytes per token row
+  static constexpr int kKxBytes = 2 * 16 * kKxRow;    // two pages per block
 
   // online-softmax state: O^T tiles, running max (log2 units) and sum per column
   f32x4 acc[NQT][NT];
@@ -385,7 +399,10 @@ struct KvUnit {
         }
       }
     } else {
-      const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
+      const int lane = n16 + 16 * j;
+      // whole lines (kKLines): token 8c + lane / 8 of the page, 16 bytes at 16 (lane % 8)
+      const uint32_t koff = kKLines ? (uint32_t)((lane >> 3) * p.k_stok32 + kvh * p.k_shead32 + 16 * (lane & 7))
+                                    : (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
       const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
 #pragma unroll
       for (int T = 0; T < 2; ++T) {
@@ -396,7 +413,9 @@ struct KvUnit {
               const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
-            r.k[T][c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * c, kStreamPolicy));
+            r.k[T][c] = __builtin_bit_cast(
+                i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, kKLines ? 8 * c * p.k_stok32 : 64 * c,
+                                                             kStreamPolicy));
         }
         if (parts & 2) {
           const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
@@ -460,11 +479,29 @@ struct KvUnit {
   // when j <= i (causal: lim is the lane column's last visible key) or when
   // bit j of the row's ancestor word is set (TREE); min_lim is the last key
   // every column sees.  after_scores() runs once r.k has been consumed.
+  // Whole-line K (kKLines) -> the MFMA layout through the wave's LDS rows kx.
+  // The writes and reads of one wave are ordered by the LDS pipeline, and the
+  // previous block's reads of kx precede these writes in program order.
+  static __device__ __forceinline__ void k_to_mfma(Block &r, char *kx, int n16, int j) {
+    const int lane = n16 + 16 * j;
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        *reinterpret_cast<i32x4 *>(kx + T * 16 * kKxRow + (8 * c + (lane >> 3)) * kKxRow + 16 * (lane & 7)) =
+            r.k[T][c];
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        r.k[T][c] = *reinterpret_cast<const i32x4 *>(kx + T * 16 * kKxRow + n16 * kKxRow + 16 * j + 64 * c);
+  }
+
   template <typename F>
   __device__ __forceinline__ void compute_block(Block &r, int pid, int blk, int tok0, int uEnd, int draft0,
                                                 const int (&lim)[TREE ? 1 : NQT], int min_lim,
                                                 const int (&tree)[TREE ? NQT : 1], const qvec8 (&qop)[NQT][NS],
-                                                float c_log2, int j, F &&after_scores) {
+                                                float c_log2, int j, char *kx, F &&after_scores) {
     // Tokens past the unit (the tail of the sequence's last page, or a tile
     // beyond the unit read from page 0) and tokens of an invalid page may hold
     // arbitrary bytes, NaN codes included: zero their V so that p = 0
@@ -499,6 +536,7 @@ struct KvUnit {
         }
       }
     }
+    if constexpr (kKLines) k_to_mfma(r, kx, (int)(threadIdx.x & 15), j);
     // ---- S^T = K . Q^T ----
     f32x4 sc[NQT][2];
 #pragma unroll
@@ -759,7 +797,7 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // fp32 partial (o / l, m, l) at its split slot.
 template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
-  typedef KvUnit<QT, KT, D, NQT, TREE> U;
+  typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128 && NB == 1> U;
   typedef typename U::qvec8 qvec8;
   typedef typename U::Block Block;
   constexpr int kTok = U::kTok;            // tokens per block
@@ -779,12 +817,15 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   __shared__ int s_seq[2];     // item number of the slot's contents
   __shared__ int s_ack[2];     // waves other than 0 that have read the slot
   __shared__ int s_prefix_ready;
+  // per-wave LDS rows of the whole-line K pass (kKLines)
+  __shared__ __attribute__((aligned(16))) char s_kx[U::kKLines ? kMaxWaves * U::kKxBytes : 16];
 
   const int nwaves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int n16 = lane & 15;
   const int j = lane >> 4;
+  char *const kx = s_kx + (U::kKLines ? wave * U::kKxBytes : 0);
   const int q_len = p.q_len;
   const int B = p.batch;
   const int S = p.split_size;
@@ -1176,7 +1217,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       U st;
       st.reset();
       auto compute_block = [&](Block &r, int blk, auto &&after_scores) {
-        st.compute_block(r, pidU, blk, uStart + kTok * blk, uEnd, draft0, lim, min_lim, treeU, qop, c_log2, j,
+        st.compute_block(r, pidU, blk, uStart + kTok * blk, uEnd, draft0, lim, min_lim, treeU, qop, c_log2, j, kx,
                          after_scores);
       };
 
