@@ -1,6 +1,7 @@
 """GPU parity over a seeded random sweep of shapes.
 
-Each case draws a batch, head layout, head_dim, q_len, cache dtype, scale
+Each case draws a batch, head layout, head_dim, q_len, cache dtype (e4m3fn, fp16,
+bf16; a second range of seeds uses e5m2 caches), scale
 kind, ragged lengths (empty sequences and page-boundary lengths included),
 split size, workspace dtype and (fp8, q_len > 1) arbitrary tree-mask words
 from a fixed seed, runs the op, and compares
@@ -17,6 +18,7 @@ import pd_helpers as H
 pytestmark = pytest.mark.gpu
 
 N_CASES = 120
+N_E5M2 = 24
 SPLITS = [64, 96, 128, 256, 512, 1024]
 HEADS = [(4, 4), (8, 2), (14, 2), (16, 8), (28, 4), (32, 4)]
 
@@ -28,8 +30,8 @@ def _require_gpu():
     import l20_paged_decode  # noqa: F401  (fails loudly if the extension is missing)
 
 
-def draw(case):
-    rng = np.random.default_rng(1000 + case)
+def draw(case, seed_base=1000):
+    rng = np.random.default_rng(seed_base + case)
     hq, hkv = HEADS[rng.integers(len(HEADS))]
     d = int(rng.choice([64, 128]))
     q_len = int(rng.choice([1, 1, 2, 4]))
@@ -56,14 +58,12 @@ def draw(case):
                 tree=bool(q_len > 1 and rng.integers(2)))
 
 
-@pytest.mark.parametrize("case", range(N_CASES))
-def test_random_shape(case):
-    c = draw(case)
+def run_case(c):
     pdt = torch.float16 if c["partial"] == "fp16" else torch.float32
-    print(case, c, flush=True)
-    if c["cache"] == "fp8":
+    if c["cache"] in ("fp8", "e5m2"):
         inp = H.make_synthetic(c["batch"], c["hq"], c["hkv"], c["d"], c["lens"], q_len=c["q_len"],
-                               per_head=c["per_head"], seed=c["seed"], garbage_tail=True)
+                               per_head=c["per_head"], seed=c["seed"], garbage_tail=True,
+                               fp8="e5m2" if c["cache"] == "e5m2" else "e4m3fn")
         if c["tree"]:  # arbitrary ancestor words over the q_len drafts, one row per (sequence, draft)
             w = np.random.default_rng(c["seed"]).integers(0, 2**32, size=(c["batch"], c["q_len"]), dtype=np.int64)
             inp["tree_mask"] = torch.from_numpy(np.where(w >= 2**31, w - 2**32, w).astype(np.int32)).cuda()
@@ -74,3 +74,18 @@ def test_random_shape(case):
                                  q_len=c["q_len"], seed=c["seed"], garbage_tail=True, csr_pad=1)
         csr = bool(c["seed"] & 1)
         H.compare(*H.run_op16(inp, c["split"], csr=csr, partial_dtype=pdt), *H.run_oracle16(inp, csr=csr))
+
+
+@pytest.mark.parametrize("case", range(N_CASES))
+def test_random_shape(case):
+    c = draw(case)
+    print(case, c, flush=True)
+    run_case(c)
+
+
+@pytest.mark.parametrize("case", range(N_E5M2))
+def test_random_shape_e5m2(case):
+    """Another seed range with OCP e5m2 caches (the draws' other fields as above)."""
+    c = dict(draw(case, seed_base=5000), cache="e5m2")
+    print(case, c, flush=True)
+    run_case(c)
