@@ -193,10 +193,10 @@ class TreeAttentionWorkspace(tuple):
             self._buffers[name] = t
         return t
 
-    def constant(self, name: str, make, shape) -> torch.Tensor:
-        """A tensor made once by ``make()`` and kept while its shape stays ``shape``."""
+    def constant(self, name: str, make, shape, device) -> torch.Tensor:
+        """A tensor made once by ``make()`` and kept while its shape and device stay."""
         t = self._buffers.get(name)
-        if t is None or tuple(t.shape) != tuple(shape):
+        if t is None or tuple(t.shape) != tuple(shape) or t.device != torch.device(device):
             t = make()
             self._buffers[name] = t
         return t
@@ -308,7 +308,7 @@ def hybrid_tree_attention_paged_prefix(
         rows_q = qb.view(entries * cols, num_q_heads, head_dim)
     pages = max(1, math.ceil(cached_length / 16))
     if contiguous_pages:
-        ramp = ws.constant("ramp", lambda: torch.arange(pages, dtype=torch.int32, device=dev), (pages,))
+        ramp = ws.constant("ramp", lambda: torch.arange(pages, dtype=torch.int32, device=dev), (pages,), dev)
         table = ws.buffer("table", (entries, pages), torch.int32, dev)
         torch.add(page_base.to(torch.int32)[:, None, None], ramp[None, None, :], out=table.view(batch, chunks, pages))
     elif chunks > 1:
@@ -365,7 +365,8 @@ def causal_verifier_attention_paged(
     if draft < 1 or draft > MAX_DRAFT:
         raise ValueError("causal verifier path supports draft_length in [1, 64]")
     ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
-    chain = ws.constant("chain_mask", lambda: make_chain_tree_mask(draft, device=query.device), (draft, draft))
+    chain = ws.constant("chain_mask", lambda: make_chain_tree_mask(draft, device=query.device), (draft, draft),
+                        query.device)
     return hybrid_tree_attention_paged_prefix(
         query, key_cache, value_cache, suffix_key, suffix_value, block_table, chain, cached_length,
         workspace=ws, block_t=block_t, k_scale=k_scale, v_scale=v_scale, split_size=split_size,
