@@ -53,6 +53,23 @@ def make_chain_tree_mask(draft_length: int, *, device=None) -> torch.Tensor:
     return positions[None, :] <= positions[:, None]
 
 
+def should_use_l20_split_tree_attention(cached_length: int) -> bool:
+    """The reference's gate between its monolithic and split (prefix summary +
+    suffix summary + merge) tree kernels (``triton_tree_attention.py:1200-1202``,
+    True from 4096 cached tokens on L20).  The MI355X path has only the split
+    form -- the prefix pass on the streaming kernel, the suffix and merge in one
+    more launch -- so it is used for every length."""
+    del cached_length
+    return True
+
+
+def l20_tree_attention_block_t(cached_length: int) -> int:
+    """The reference's Triton tile policy (``triton_tree_attention.py:1205-1207``):
+    128 from 4096 cached tokens, else 64.  The HIP kernels' tiling is fixed; the
+    entry points accept and validate ``block_t`` for call compatibility."""
+    return 128 if cached_length >= 4096 else 64
+
+
 def tree_mask_bits(ancestor_mask: torch.Tensor) -> torch.Tensor:
     """Boolean ancestor mask ``[..., S, S]`` (row i sees draft j) -> int32 bitmasks
     ``[..., S]`` with bit j of word i set iff ``ancestor_mask[..., i, j]``; S <= 32."""

@@ -66,3 +66,13 @@ def test_workspace_layout():
     ws = tv.allocate_tree_attention_workspace(q)
     assert [tuple(t.shape) for t in ws] == [(2, 5, 8, 64), (2, 5, 8), (2, 5, 8)] * 2
     assert all(t.dtype == torch.float32 for t in ws)
+
+
+def test_reference_policy_helpers():
+    import l20_tree_verify as tv
+
+    # the split form is the only MI355X tree path; the tile policy keeps the reference's values
+    assert all(tv.should_use_l20_split_tree_attention(n) for n in (0, 1, 4095, 4096, 131072))
+    assert [tv.l20_tree_attention_block_t(n) for n in (0, 4095, 4096, 100000)] == [64, 64, 128, 128]
+    for n in (0, 4095, 4096):
+        tv._check_block_t(tv.l20_tree_attention_block_t(n))  # accepted by the entry points
