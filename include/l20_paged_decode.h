@@ -75,7 +75,9 @@ enum l20_pd_status {
  *                  with page_indptr [batch+1] (CSR), the flat page list: sequence b's
  *                  pages are block_table[page_indptr[b] .. page_indptr[b+1])
  *   seq_lens       [batch]  int32, each <= max_seq_len, includes the q_len new tokens
- *   partial_output [batch*q_len, num_q_heads, >= num_splits, head_dim]  fp32 or fp16
+ *   partial_output [batch*q_len, num_q_heads, >= num_splits, head_dim]  fp32, fp16 or bf16
+ *                  (bf16: what the reference's hook-facing allocator gives a bf16 query,
+ *                  integrations/vllm/l20_paged_split_kv.py:24-26)
  *   partial_max/sum[batch*q_len, num_q_heads, >= num_splits]  fp32
  *   output         [batch*q_len, num_q_heads, head_dim]  same dtype as query
  *   lse            [batch*q_len, num_q_heads] fp32 natural-log LSE, or NULL

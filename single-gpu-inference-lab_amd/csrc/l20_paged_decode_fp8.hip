@@ -106,7 +106,7 @@ struct PartialParams {
   const float *v_scale_ph;
   float qk_scale_log2;  // softmax_scale * log2(e)
   int q_len, num_q_heads, num_kv_heads, group, split_size, num_splits;
-  int po_f32;
+  int po_kind;  // partial o/l element: 0 fp32, 1 fp16, 2 bf16
   int l_cap;  // min(num_splits * split_size, block-table pages * 16): tokens past it are never touched
   int batch;
   int bt_pages;  // block-table row length
@@ -727,23 +727,29 @@ struct KvUnit {
         const int64_t po_idx = prow * p.po_srow + h * p.po_shead + slot_split * p.po_ssplit + DPL * j;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          if (p.po_f32) {
+          if (p.po_kind == 0) {
             float *dst = reinterpret_cast<float *>(p.po) + po_idx + rr * NT;
 #pragma unroll
             for (int t = 0; t < NT; t += 4)
               *reinterpret_cast<f32x4 *>(dst + t) = f32x4{acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv,
                                                           acc[qt][t + 2][rr] * inv, acc[qt][t + 3][rr] * inv};
           } else {
+            // 16-bit partials: 2 bytes per element at the same element offsets
             _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx + rr * NT;
+            const bool bf = p.po_kind == 2;
             if constexpr (D == 128) {
               i32x4 w;
 #pragma unroll
-              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+              for (int t = 0; t < NT; t += 2)
+                w[t >> 1] = bf ? pack2<__bf16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv)
+                               : pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
               *reinterpret_cast<i32x4 *>(dst) = w;
             } else {
               i32x2 w;
 #pragma unroll
-              for (int t = 0; t < NT; t += 2) w[t >> 1] = pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
+              for (int t = 0; t < NT; t += 2)
+                w[t >> 1] = bf ? pack2<__bf16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv)
+                               : pack2<_Float16>(acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv);
               *reinterpret_cast<i32x2 *>(dst) = w;
             }
           }
@@ -1312,6 +1318,23 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
 // ---------------------------------------------------------------------------
 // LSE merge kernel
 // ---------------------------------------------------------------------------
+// Eight consecutive partial o/l elements at element offset off, as fp32.
+__device__ __forceinline__ void load_partial8(const void *po, int kind, int64_t off, f32x4 &a, f32x4 &b) {
+  if (kind == 0) {
+    const float *src = reinterpret_cast<const float *>(po) + off;
+    a = *reinterpret_cast<const f32x4 *>(src);
+    b = *reinterpret_cast<const f32x4 *>(src + 4);
+  } else if (kind == 1) {
+    const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(po) + off);
+    a = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    b = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+  } else {
+    const bf16x8 v = *reinterpret_cast<const bf16x8 *>(reinterpret_cast<const __bf16 *>(po) + off);
+    a = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    b = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+  }
+}
+
 struct MergeParams {
   const void *po;
   int64_t po_srow, po_shead, po_ssplit;
@@ -1324,7 +1347,7 @@ struct MergeParams {
   int64_t o_srow, o_shead;
   float *lse;
   int64_t lse_srow, lse_shead;
-  int q_len, split_size, num_splits, po_f32;
+  int q_len, split_size, num_splits, po_kind;  // po_kind as in PartialParams
   int l_cap;  // same clamp as the partial kernel
   int rows, num_q_heads;
 };
@@ -1384,15 +1407,7 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
       ms[k] = pm[(int64_t)sl * p.pm_ssplit];
       ls[k] = pl[(int64_t)sl * p.pl_ssplit];
       const int64_t off = base + (int64_t)sl * p.po_ssplit;
-      if (p.po_f32) {
-        const float *src = reinterpret_cast<const float *>(p.po) + off;
-        o0[k] = *reinterpret_cast<const f32x4 *>(src);
-        o1[k] = *reinterpret_cast<const f32x4 *>(src + 4);
-      } else {
-        const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(p.po) + off);
-        o0[k] = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-        o1[k] = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
-      }
+      load_partial8(p.po, p.po_kind, off, o0[k], o1[k]);
     }
 #pragma unroll
     for (int k = 0; k < kSteps; ++k) {
@@ -1487,15 +1502,7 @@ __global__ __launch_bounds__(256) void pd_merge_narrow(MergeParams p) {
       ms[s] = pm[(int64_t)s * p.pm_ssplit];
       ls[s] = pl[(int64_t)s * p.pl_ssplit];
       const int64_t off = base + (int64_t)s * p.po_ssplit;
-      if (p.po_f32) {
-        const float *src = reinterpret_cast<const float *>(p.po) + off;
-        o0[s] = *reinterpret_cast<const f32x4 *>(src);
-        o1[s] = *reinterpret_cast<const f32x4 *>(src + 4);
-      } else {
-        const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(p.po) + off);
-        o0[s] = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-        o1[s] = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
-      }
+      load_partial8(p.po, p.po_kind, off, o0[s], o1[s]);
     }
   }
   const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
@@ -1657,8 +1664,8 @@ int32_t check_args(const l20_pd_fp8_args *a) {
     if (!a->partial_output || !a->partial_max || !a->partial_sum)
       return fail(L20_PD_EINVAL, "partial output workspace has wrong shape");
     if (a->partial_splits < n_s) return fail(L20_PD_EINVAL, "partial output workspace has wrong shape");
-    if (a->partial_dtype != L20_PD_FP32 && a->partial_dtype != L20_PD_FP16)
-      return fail(L20_PD_EINVAL, "partial output must be fp32 or fp16");
+    if (a->partial_dtype != L20_PD_FP32 && a->partial_dtype != L20_PD_FP16 && a->partial_dtype != L20_PD_BF16)
+      return fail(L20_PD_EINVAL, "partial output must be fp32, fp16 or bf16");
   }
   for (int which = 0; which < 2; ++which) {
     const int64_t st = which ? a->v_stride_token : a->k_stride_token;
@@ -1680,10 +1687,10 @@ int32_t check_args(const l20_pd_fp8_args *a) {
     return fail(L20_PD_EINVAL, "query pointer and strides must be 16-byte aligned");
   if (((uintptr_t)a->output % 16) != 0 || (a->o_stride_row % 8) != 0 || (a->o_stride_head % 8) != 0)
     return fail(L20_PD_EINVAL, "output pointer and strides must be 16-byte aligned");
-  if (n_s > 1 && a->partial_dtype == L20_PD_FP16 &&
+  if (n_s > 1 && a->partial_dtype != L20_PD_FP32 &&
       (((uintptr_t)a->partial_output % 16) != 0 || a->po_stride_row % 8 || a->po_stride_head % 8 ||
        a->po_stride_split % 8))
-    return fail(L20_PD_EINVAL, "fp16 partial output must be 16-byte aligned");
+    return fail(L20_PD_EINVAL, "16-bit partial output must be 16-byte aligned");
   if (n_s > 1 && a->partial_dtype == L20_PD_FP32 &&
       (((uintptr_t)a->partial_output % 16) != 0 || a->po_stride_row % 4 || a->po_stride_head % 4 ||
        a->po_stride_split % 4))
@@ -1873,7 +1880,7 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.group = a.num_q_heads / a.num_kv_heads;
   pp.split_size = a.split_size;
   pp.num_splits = n_s > 0 ? n_s : 1;
-  pp.po_f32 = a.partial_dtype == L20_PD_FP32;
+  pp.po_kind = a.partial_dtype == L20_PD_FP32 ? 0 : a.partial_dtype == L20_PD_FP16 ? 1 : 2;
   pp.l_cap = length_cap(a, pp.num_splits);
   pp.batch = a.batch;
   pp.bt_pages = a.bt_max_pages;
@@ -1958,7 +1965,7 @@ l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
   mp.q_len = a.q_len;
   mp.split_size = a.split_size;
   mp.num_splits = num_splits;
-  mp.po_f32 = a.partial_dtype == L20_PD_FP32;
+  mp.po_kind = a.partial_dtype == L20_PD_FP32 ? 0 : a.partial_dtype == L20_PD_FP16 ? 1 : 2;
   mp.l_cap = length_cap(a, num_splits);
   mp.rows = a.batch * a.q_len;
   mp.num_q_heads = a.num_q_heads;

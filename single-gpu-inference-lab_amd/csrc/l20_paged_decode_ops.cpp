@@ -104,8 +104,9 @@ l20_pd_fp8_args make_args(const at::Tensor &query, const at::Tensor &key_cache, 
                     partial_output.size(2) >= n_s && partial_output.size(3) == head_dim &&
                     partial_output.stride(3) == 1,
                 "partial output workspace has wrong shape");
-    TORCH_CHECK(partial_output.scalar_type() == at::kFloat || partial_output.scalar_type() == at::kHalf,
-                "partial output workspace must be fp32 or fp16");
+    TORCH_CHECK(partial_output.scalar_type() == at::kFloat || partial_output.scalar_type() == at::kHalf ||
+                    partial_output.scalar_type() == at::kBFloat16,
+                "partial output workspace must be fp32, fp16 or bf16");
     for (const at::Tensor *t : {&partial_max, &partial_sum}) {
       TORCH_CHECK(t->dim() == 3 && t->size(0) == rows && t->size(1) == heads && t->size(2) >= n_s &&
                       t->scalar_type() == at::kFloat,

@@ -598,3 +598,36 @@ def test_mixed_fp8_formats_are_rejected():
         torch.ops.l20_stack.paged_decode_fp8_e4m3_split_out(
             inp["query"], inp["key_cache"], v5, inp["block_table"], inp["seq_lens"], po, pm, ps,
             torch.empty_like(inp["query"]), 1.0, 1.0, inp["max_seq_len"], 64)
+
+
+# ------------------------------------------------------------ the reference allocator's workspace
+def test_reference_allocator_workspace_bf16_partials():
+    """A workspace laid out as the reference's allocate_l20_paged_split_kv_workspace
+    makes it (integrations/vllm/l20_paged_split_kv.py:14-30: partial_output in the
+    query dtype, next_pow2(ceil(max_seq_len / split)) splits) works as given."""
+    from l20_paged_split_kv import l20_paged_split_kv_attention_fp8
+
+    inp = H.make_synthetic(6, 28, 4, 128, [3000, 17, 700, 1, 1500, 2049], seed=61)
+    exp = H.run_oracle(inp)
+    q = inp["query"]
+    n_s = 1 << (-(-inp["max_seq_len"] // 512) - 1).bit_length()  # next power of two: 6 -> 8
+    assert n_s == 8
+    ws = (torch.empty(q.shape[0], q.shape[1], n_s, 128, dtype=q.dtype, device="cuda"),
+          torch.empty(q.shape[0], q.shape[1], n_s, device="cuda"),
+          torch.empty(q.shape[0], q.shape[1], n_s, device="cuda"),
+          torch.empty_like(q))
+    out = l20_paged_split_kv_attention_fp8(q, inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                           inp["seq_lens"], k_scale=inp["k_scale"], v_scale=inp["v_scale"],
+                                           max_seq_len=inp["max_seq_len"], split_size=512, workspace=ws)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == ws[3].data_ptr()
+    H.compare(out, None, exp[0], exp[1], check_lse=False)
+
+
+@pytest.mark.parametrize("case", EDGE[:4], ids=[e[0] for e in EDGE[:4]])
+@pytest.mark.parametrize("split", [64, 1024])
+def test_bf16_partial_workspace(case, split):
+    _, batch, hq, hkv, d, lens, q_len, per_head, dtype = case
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, per_head=per_head, dtype=dtype,
+                           seed=zlib.crc32(case[0].encode()) % 1000 + 3, garbage_tail=True)
+    H.compare(*H.run_op(inp, split, partial_dtype=torch.bfloat16), *H.run_oracle(inp))
