@@ -6,6 +6,7 @@ reference's vLLM-facing module ``integrations/vllm/l20_paged_split_kv.py``
 
 * ``allocate_l20_paged_split_kv_workspace`` (``:14-30``)
 * ``l20_paged_split_kv_attention_fp8``     (``:597-695``)
+* ``l20_paged_split_kv_attention``         (``:491-595``, fp16/bf16 caches)
 * ``should_use_l20_paged_fp8_split_kv``    (``:705-709``)
 
 but runs the hand-written HIP kernels behind
@@ -142,6 +143,80 @@ def l20_paged_split_kv_attention_fp8(
         partial_output, partial_max, partial_sum, output,
         ks, vs, int(max_seq_len), int(split_size),
         softmax_scale, ks_ph, vs_ph, int(q_len), lse,
+    )
+
+
+def l20_paged_split_kv_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    split_size: Optional[int] = 512,
+    workspace: Optional[Workspace] = None,
+    page_granular: bool = False,
+    grouped_gqa: bool = False,
+    max_seq_len: Optional[int] = None,
+    output: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    q_len: int = 1,
+    lse: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Paged decode attention over fp16/bf16 caches (the query's dtype); returns the
+    output ([B*q_len, Hq, D]).  The reference's 16-bit hook-facing function
+    (``l20_paged_split_kv.py:491-595``) with its names, keywords and errors,
+    running ``torch.ops.l20_stack.paged_decode_split_out``.  ``page_granular``
+    and ``grouped_gqa`` choose between the reference's Triton kernel variants;
+    the HIP kernel has one form, so they are accepted and change nothing.
+    ``max_seq_len`` (default: ``seq_lens.max()``, a host read as in the
+    reference), ``output``, ``softmax_scale``, ``q_len`` and ``lse`` are the
+    fp8 function's extensions."""
+    del page_granular, grouped_gqa
+    if not is_mi355x(query.device):
+        raise RuntimeError("requires an MI355X (gfx950) GPU")
+    if query.ndim != 3 or key_cache.ndim != 4 or value_cache.shape != key_cache.shape:
+        raise RuntimeError("expected Q=[B,H,D], cache=[pages,page,Hkv,D]")
+    rows, num_q_heads, head_dim = query.shape
+    _, page_size, num_kv_heads, cache_dim = key_cache.shape
+    batch = rows // q_len if q_len > 0 else -1
+    if (
+        head_dim not in (64, 128)
+        or cache_dim != head_dim
+        or page_size != 16
+        or num_q_heads % num_kv_heads
+        or q_len < 1
+        or rows % q_len
+        or block_table.shape[0] != batch
+        or seq_lens.numel() != batch
+    ):
+        raise RuntimeError("requires compatible head_dim=64/128, 16-token-page GQA tensors")
+    if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
+        raise RuntimeError("K/V cache must have the query's dtype (fp16 or bf16)")
+    if max_seq_len is None:
+        max_seq_len = int(seq_lens.max().item()) if seq_lens.numel() else 0
+    if split_size is None:
+        split_size = default_split_size(batch, num_kv_heads, max_seq_len, query.device)
+    num_splits = _num_splits(max_seq_len, split_size)
+    if workspace is None:
+        workspace = allocate_l20_paged_split_kv_workspace(query, max_seq_len, split_size=split_size)
+    partial_output, partial_max, partial_sum, workspace_output = workspace
+    if output is None:
+        output = workspace_output
+    if (
+        tuple(partial_output.shape[:2]) != (rows, num_q_heads)
+        or partial_output.shape[2] < num_splits
+        or partial_output.shape[3] != head_dim
+        or tuple(partial_max.shape[:2]) != (rows, num_q_heads)
+        or partial_max.shape[2] < num_splits
+        or partial_sum.shape != partial_max.shape
+        or output.shape != query.shape
+    ):
+        raise RuntimeError("paged split-KV workspace shape does not match the request")
+    return torch.ops.l20_stack.paged_decode_split_out(
+        query, key_cache, value_cache, block_table, seq_lens,
+        partial_output, partial_max, partial_sum, output,
+        int(max_seq_len), int(split_size), softmax_scale, int(q_len), lse,
     )
 
 

@@ -631,3 +631,22 @@ def test_bf16_partial_workspace(case, split):
     inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, per_head=per_head, dtype=dtype,
                            seed=zlib.crc32(case[0].encode()) % 1000 + 3, garbage_tail=True)
     H.compare(*H.run_op(inp, split, partial_dtype=torch.bfloat16), *H.run_oracle(inp))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_16bit_hook_facing_function(dtype):
+    """l20_paged_split_kv_attention (the reference's 16-bit entry, l20_paged_split_kv.py:491-595):
+    its keywords, a reused reference-shaped workspace, and the Triton-variant knobs accepted."""
+    from l20_paged_split_kv import allocate_l20_paged_split_kv_workspace, l20_paged_split_kv_attention
+
+    inp = H.make_synthetic16(5, 16, 2, 128, [2049, 1, 700, 0, 1300], dtype=dtype, seed=71)
+    exp = H.run_oracle16(inp)
+    ws = allocate_l20_paged_split_kv_workspace(inp["query"], inp["max_seq_len"], split_size=512)
+    for kw in ({}, {"page_granular": True}, {"grouped_gqa": True}):
+        out = l20_paged_split_kv_attention(inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                           inp["seq_lens"], split_size=512, workspace=ws, **kw)
+        torch.cuda.synchronize()
+        H.compare(out, None, exp[0], exp[1], check_lse=False)
+    with pytest.raises(RuntimeError, match="query's dtype"):
+        l20_paged_split_kv_attention(inp["query"], inp["key_cache"].float(), inp["value_cache"].float(),
+                                     inp["block_table"], inp["seq_lens"])
