@@ -380,3 +380,23 @@ def test_hybrid_contiguous_pages_equal_block_table():
         tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, block_t=48)
     with pytest.raises(ValueError, match="page_base"):
         tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, contiguous_pages=True)
+
+
+def test_dispatch_helpers_route_to_the_hybrid_and_causal_paths(monkeypatch):
+    import l20_tree_attention_dispatch as disp
+    import l20_tree_verify as tv
+
+    x = _hybrid_inputs(2, 16, 4, 128, 4100, 6, seed=17)
+    args = (x["query"], x["kc"], x["vc"], x["sk"], x["sv"], x["table"])
+    monkeypatch.delenv(disp.ENABLE_ENV, raising=False)
+    assert disp.maybe_l20_tree_attention(*args, x["mask"], 4100) is None
+    monkeypatch.setenv(disp.ENABLE_ENV, "1")
+    got = disp.maybe_l20_tree_attention(*args, x["mask"], 4100)
+    want = tv.hybrid_tree_attention_paged_prefix(*args, x["mask"], 4100)
+    torch.cuda.synchronize()
+    assert got is not None and torch.equal(got, want)
+    got_c = disp.maybe_l20_causal_verifier_attention(*args, 4100)
+    want_c = tv.causal_verifier_attention_paged(*args, 4100)
+    torch.cuda.synchronize()
+    assert got_c is not None and torch.equal(got_c, want_c)
+    assert disp.maybe_l20_tree_attention(*args, x["mask"], 1000) is None  # below the threshold
