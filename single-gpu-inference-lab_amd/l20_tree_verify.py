@@ -19,7 +19,8 @@ Two entry points:
   ancestor bitmasks (``tree_mask``): each K/V page is read once per KV head for
   all S x GQA-group query columns.  Requires S x group <= 32 and S <= 32.
 * ``hybrid_tree_attention_paged_prefix`` / ``causal_verifier_attention_paged``
-  -- the reference's signatures, with the drafts' K/V in separate contiguous
+  (and the contiguous-cache ``hybrid_tree_attention`` / ``hybrid_tree_attention_split``,
+  which view or copy the K/V into 16-token pages first) -- the reference's signatures, with the drafts' K/V in separate contiguous
   ``[B, S, Hkv, D]`` tensors next to a paged prefix of ``cached_length``
   tokens.  The prefix pass (the HBM-bound part) runs on the HIP kernel with
   every draft row a query column and returns its LSE; ``l20_pd_tree_suffix_merge``
@@ -388,3 +389,81 @@ def causal_verifier_attention_paged(
         query, key_cache, value_cache, suffix_key, suffix_value, block_table, chain, cached_length,
         workspace=ws, block_t=block_t, k_scale=k_scale, v_scale=v_scale, split_size=split_size,
         softmax_scale=softmax_scale, output=output)
+
+
+def _validate_contiguous(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, ancestor_mask: torch.Tensor,
+                         cached_length: int) -> None:
+    """The reference's checks of the contiguous-cache entry points
+    (``triton_tree_attention.py:683-703``), head_dim 64 also allowed."""
+    if query.ndim != 4 or key.ndim != 4 or value.shape != key.shape:
+        raise ValueError("expected query=[B,S,Hq,D], key/value=[B,T,Hkv,D]")
+    if ancestor_mask.ndim != 2:
+        raise ValueError("expected ancestor_mask=[S,S]")
+    batch, draft_length, num_q_heads, head_dim = query.shape
+    key_batch, total_length, num_kv_heads, key_dim = key.shape
+    if key_batch != batch or key_dim != head_dim:
+        raise ValueError("query and KV dimensions do not match")
+    if total_length != cached_length + draft_length:
+        raise ValueError("KV length must equal cached_length + draft_length")
+    if ancestor_mask.shape != (draft_length, draft_length):
+        raise ValueError("ancestor_mask must match draft_length")
+    if head_dim not in (64, 128):
+        raise ValueError("head_dim must be 64 or 128")
+    if num_q_heads % num_kv_heads:
+        raise ValueError("requires an integral GQA ratio")
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise ValueError("key/value must have the query's dtype (fp16 or bf16)")
+
+
+def _as_pages(x: torch.Tensor, ws: TreeAttentionWorkspace, name: str) -> torch.Tensor:
+    """[B, T, H, D] as a [B * ceil(T / 16), 16, H, D] page pool (sequence b on pages
+    b * ceil(T / 16) ...): a view when x is contiguous and T is a multiple of 16,
+    else a copy into a workspace buffer.  Tokens past a sequence's length in its
+    last page (the copy's unwritten tail, or the view's suffix tokens during the
+    prefix pass) are loaded but masked: score -inf, V zeroed."""
+    batch, total, heads, dim = x.shape
+    pages = -(-total // 16)
+    if x.is_contiguous() and total % 16 == 0:
+        return x.view(batch * pages, 16, heads, dim)
+    buf = ws.buffer(name, (batch * pages, 16, heads, dim), x.dtype, x.device)
+    buf.view(batch, pages * 16, heads, dim)[:, :total].copy_(x)
+    return buf
+
+
+def _contiguous_tree(query, key, value, ancestor_mask, cached_length, ws, block_t, softmax_scale, output):
+    _validate_contiguous(query, key, value, ancestor_mask, cached_length)
+    batch, total = key.shape[0], key.shape[1]
+    pages = -(-total // 16)
+    kp = _as_pages(key, ws, "key_pages")
+    vp = _as_pages(value, ws, "value_pages")
+    table = ws.constant("contiguous_table",
+                        lambda: torch.arange(batch * pages, dtype=torch.int32, device=query.device).view(batch, pages),
+                        (batch, pages), query.device)
+    return hybrid_tree_attention_paged_prefix(
+        query, kp, vp, key[:, cached_length:], value[:, cached_length:], table, ancestor_mask, cached_length,
+        workspace=ws, block_t=block_t, softmax_scale=softmax_scale, output=output)
+
+
+def hybrid_tree_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, ancestor_mask: torch.Tensor,
+                          cached_length: int, *, block_t: Optional[int] = None,
+                          softmax_scale: Optional[float] = None) -> torch.Tensor:
+    """Tree attention over contiguous K/V [B, cached_length + S, Hkv, D] (the
+    reference's ``hybrid_tree_attention``, ``triton_tree_attention.py:706-758``):
+    every draft row sees the cached prefix, draft j iff ``ancestor_mask[i, j]``.
+    Runs the paged path: the prefix as 16-token pages of the same memory, the
+    last S tokens as the suffix."""
+    _check_block_t(block_t)
+    return _contiguous_tree(query, key, value, ancestor_mask, cached_length,
+                            allocate_tree_attention_workspace(query), block_t, softmax_scale, None)
+
+
+def hybrid_tree_attention_split(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                ancestor_mask: torch.Tensor, cached_length: int, *, workspace=None,
+                                block_t: Optional[int] = None, softmax_scale: Optional[float] = None,
+                                output: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference's prefix/suffix-summary form (``triton_tree_attention.py:779-886``)
+    of ``hybrid_tree_attention``; a ``TreeAttentionWorkspace`` keeps its buffers
+    between calls."""
+    _check_block_t(block_t)
+    ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
+    return _contiguous_tree(query, key, value, ancestor_mask, cached_length, ws, block_t, softmax_scale, output)

@@ -400,3 +400,45 @@ def test_dispatch_helpers_route_to_the_hybrid_and_causal_paths(monkeypatch):
     torch.cuda.synchronize()
     assert got_c is not None and torch.equal(got_c, want_c)
     assert disp.maybe_l20_tree_attention(*args, x["mask"], 1000) is None  # below the threshold
+
+
+CONTIG = [
+    # batch, hq, hkv, d, cached, draft, dtype, layout
+    (2, 16, 4, 128, 1020, 4, torch.bfloat16, "contiguous"),   # T = 1024: pages are a view
+    (2, 28, 4, 128, 777, 8, torch.bfloat16, "contiguous"),    # T % 16 != 0: copied into pages
+    (3, 8, 8, 64, 300, 5, torch.float16, "strided"),          # a slice of a wider tensor: copied
+    (1, 8, 2, 128, 0, 3, torch.bfloat16, "contiguous"),       # no cached prefix
+]
+
+
+@pytest.mark.parametrize("case", CONTIG, ids=[f"c{i}" for i in range(len(CONTIG))])
+def test_contiguous_cache_tree_attention(case):
+    """hybrid_tree_attention / hybrid_tree_attention_split (the reference's contiguous-cache
+    entry points, triton_tree_attention.py:706-886) against the fp64 dense oracle."""
+    import l20_tree_verify as tv
+
+    batch, hq, hkv, d, cached, draft, dtype, layout = case
+    total = cached + draft
+    g = torch.Generator().manual_seed(cached + draft)
+    query = torch.randn(batch, draft, hq, d, generator=g).to(dtype)
+    if layout == "strided":
+        wide_k = torch.randn(batch, total, hkv, 2 * d, generator=g).to(dtype)
+        wide_v = torch.randn(batch, total, hkv, 2 * d, generator=g).to(dtype)
+        key, value = wide_k.cuda()[..., :d], wide_v.cuda()[..., :d]
+        assert not key.is_contiguous()
+    else:
+        key = torch.randn(batch, total, hkv, d, generator=g).to(dtype).cuda()
+        value = torch.randn(batch, total, hkv, d, generator=g).to(dtype).cuda()
+    mask = torch.from_numpy(random_tree(draft, np.random.default_rng(draft)))
+    kf, vf = key.float().cpu().numpy(), value.float().cpu().numpy()
+    exp = _dense_oracle(query.float().numpy(), kf[:, :cached], vf[:, :cached], kf[:, cached:], vf[:, cached:],
+                        mask.numpy(), d ** -0.5)
+    a = tv.hybrid_tree_attention(query.cuda(), key, value, mask.cuda(), cached)
+    ws = tv.allocate_tree_attention_workspace(query.cuda())
+    b = tv.hybrid_tree_attention_split(query.cuda(), key, value, mask.cuda(), cached, workspace=ws, block_t=64)
+    b2 = tv.hybrid_tree_attention_split(query.cuda(), key, value, mask.cuda(), cached, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(b, b2)
+    assert np.abs(a.float().cpu().numpy() - exp).max() <= H.OUT_ATOL
+    with pytest.raises(ValueError, match="cached_length"):
+        tv.hybrid_tree_attention(query.cuda(), key, value, mask.cuda(), cached + 1)
