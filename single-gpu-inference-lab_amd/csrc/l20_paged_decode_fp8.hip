@@ -23,7 +23,9 @@
 //    A sequence with a single split writes the final output and LSE;
 //    otherwise the fp32 partial (O / l, m, l) goes to the caller's workspace.
 //
-//  pd_merge<QT, D, WPP>   WPP waves per (query row, q head), WPP from the split count.
+//  pd_merge<QT, D, WPP, PK>   WPP waves per (query row, q head), WPP from the split
+//    count; PK the partial element (0 fp32, 1 fp16, 2 bf16).  pd_merge_narrow<QT, D, PK>
+//    for at most eight splits and many pairs.
 //    LSE merge of a row's splits: M = max m_s, w_s = 2^(m_s - M) l_s,
 //    out = sum w_s o_s / sum w_s, lse = ln2 (M + log2 sum w_s).
 //
@@ -1318,13 +1320,17 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
 // ---------------------------------------------------------------------------
 // LSE merge kernel
 // ---------------------------------------------------------------------------
-// Eight consecutive partial o/l elements at element offset off, as fp32.
-__device__ __forceinline__ void load_partial8(const void *po, int kind, int64_t off, f32x4 &a, f32x4 &b) {
-  if (kind == 0) {
+// Eight consecutive partial o/l elements at element offset off, as fp32.  PK
+// is a template argument: a run-time choice between the three loads puts a
+// branch around each one, and the compiler then waits for every load before
+// issuing the next (eight dependent round trips in the narrow merge).
+template <int PK>
+__device__ __forceinline__ void load_partial8(const void *po, int64_t off, f32x4 &a, f32x4 &b) {
+  if constexpr (PK == 0) {
     const float *src = reinterpret_cast<const float *>(po) + off;
     a = *reinterpret_cast<const f32x4 *>(src);
     b = *reinterpret_cast<const f32x4 *>(src + 4);
-  } else if (kind == 1) {
+  } else if constexpr (PK == 1) {
     const f16x8 v = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const _Float16 *>(po) + off);
     a = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
     b = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
@@ -1358,7 +1364,7 @@ struct MergeParams {
 // a pair takes slots (w + WPP * step) * G + g, G = 512/D groups, so every load
 // of a wave is independent and issued together.  Each wave folds its groups
 // with shuffles; with WPP > 1 the pair's waves then combine through LDS.
-template <typename QT, int D, int WPP>
+template <typename QT, int D, int WPP, int PK>
 __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams p) {
   constexpr int CH = D / 8;                // 8-dim chunks per row
   constexpr int SG = 64 / CH;              // slot groups per wave
@@ -1371,10 +1377,11 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   const int wp = wave % WPP;
   const int c = lane % CH;
   const int g = lane / CH;
-  const int64_t pair = (int64_t)blockIdx.x * PPB + wave / WPP;
-  const bool live = pair < (int64_t)p.rows * p.num_q_heads;
-  const int row = live ? (int)(pair / p.num_q_heads) : 0;
-  const int h = live ? (int)(pair - (int64_t)row * p.num_q_heads) : 0;
+  // (row, head) pairs number below 2^31 (host check): 32-bit division
+  const uint32_t pair = blockIdx.x * (uint32_t)PPB + (uint32_t)(wave / WPP);
+  const bool live = pair < (uint32_t)(p.rows * p.num_q_heads);
+  const int row = live ? (int)(pair / (uint32_t)p.num_q_heads) : 0;
+  const int h = live ? (int)(pair - (uint32_t)row * (uint32_t)p.num_q_heads) : 0;
   int n = 0;
   if (live) {
     const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
@@ -1385,7 +1392,11 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
   // Online merge (max, weight sum, weighted rows) over the lane's slots; NaN
   // slots (a run continued from an earlier slot) never enter the sums.
-  const bool final_row = n > 1 && pm[0] == INFINITY;  // one run wrote the whole row already
+  // final_row: one run wrote the whole row already (slot 0's m is +inf).  Only
+  // lanes g == 0 of wave 0 of the pair write, and their first step loads slot
+  // 0, so they take it from there rather than from a load of its own (which
+  // the first step's loads would wait for).
+  bool final_row = false;
   float mx = -INFINITY, wsum = 0.0f;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
@@ -1407,8 +1418,9 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
       ms[k] = pm[(int64_t)sl * p.pm_ssplit];
       ls[k] = pl[(int64_t)sl * p.pl_ssplit];
       const int64_t off = base + (int64_t)sl * p.po_ssplit;
-      load_partial8(p.po, p.po_kind, off, o0[k], o1[k]);
+      load_partial8<PK>(p.po, off, o0[k], o1[k]);
     }
+    if (s0 == 0 && ms[0] == INFINITY) final_row = true;
 #pragma unroll
     for (int k = 0; k < kSteps; ++k) {
       if (s0 + k * WPP * SG + g < n_here && ms[k] == ms[k] && ms[k] != -INFINITY) {
@@ -1477,33 +1489,35 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
 // Narrow merge for at most kNarrowSlots split slots: lane l owns dims
 // [8c, 8c + 8) of one (query row, q head) pair (c = l % (D/8); 64 / (D/8)
 // pairs per wave) across every slot of it, so the fold needs no shuffles.
-// All slots below num_splits are read in the round trip that fetches the
-// sequence length (slots at or past the row's split count hold whatever an
-// earlier call left and are not folded).
+// NSL (2, 4 or 8) slots are read in the round trip that fetches the sequence
+// length, with no branch around any load: a slot at or past num_splits reads
+// slot 0 again (NSL is the smallest of the three >= num_splits), and slots at
+// or past the row's split count hold whatever an earlier call left and are
+// not folded.
 constexpr int kNarrowSlots = 8;
-template <typename QT, int D>
+template <typename QT, int D, int PK, int NSL>
 __global__ __launch_bounds__(256) void pd_merge_narrow(MergeParams p) {
   constexpr int CH = D / 8;     // 8-dim chunks per row
   constexpr int PPW = 64 / CH;  // pairs per wave
+  static_assert(NSL <= kNarrowSlots, "narrow merge slots");
   const int lane = threadIdx.x & 63;
   const int c = lane % CH;
-  const int64_t pair = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * PPW + lane / CH;
-  if (pair >= (int64_t)p.rows * p.num_q_heads) return;
-  const int row = (int)(pair / p.num_q_heads);
-  const int h = (int)(pair - (int64_t)row * p.num_q_heads);
+  // (row, head) pairs number below 2^31 (host check): 32-bit division
+  const uint32_t pair = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * PPW + lane / CH;
+  if (pair >= (uint32_t)(p.rows * p.num_q_heads)) return;
+  const int row = (int)(pair / (uint32_t)p.num_q_heads);
+  const int h = (int)(pair - (uint32_t)row * (uint32_t)p.num_q_heads);
   const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
   const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
   const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
-  float ms[kNarrowSlots], ls[kNarrowSlots];
-  f32x4 o0[kNarrowSlots], o1[kNarrowSlots];
+  float ms[NSL], ls[NSL];
+  f32x4 o0[NSL], o1[NSL];
 #pragma unroll
-  for (int s = 0; s < kNarrowSlots; ++s) {
-    if (s < p.num_splits) {
-      ms[s] = pm[(int64_t)s * p.pm_ssplit];
-      ls[s] = pl[(int64_t)s * p.pl_ssplit];
-      const int64_t off = base + (int64_t)s * p.po_ssplit;
-      load_partial8(p.po, p.po_kind, off, o0[s], o1[s]);
-    }
+  for (int s = 0; s < NSL; ++s) {
+    const int sl = s < p.num_splits ? s : 0;
+    ms[s] = pm[(int64_t)sl * p.pm_ssplit];
+    ls[s] = pl[(int64_t)sl * p.pl_ssplit];
+    load_partial8<PK>(p.po, base + (int64_t)sl * p.po_ssplit, o0[s], o1[s]);
   }
   const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
   const int n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
@@ -1512,7 +1526,7 @@ __global__ __launch_bounds__(256) void pd_merge_narrow(MergeParams p) {
   float mx = -INFINITY, wsum = 0.0f;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < kNarrowSlots; ++s) {
+  for (int s = 0; s < NSL; ++s) {
     if (s < n && ms[s] == ms[s] && ms[s] != -INFINITY) {
       const float m_new = fmaxf(mx, ms[s]);
       const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
@@ -1652,6 +1666,8 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (a->batch < 0 || a->max_seq_len < 0) return fail(L20_PD_EINVAL, "batch and max_seq_len must be >= 0");
   if (a->batch > 65535 || l20_pd_num_splits(a->max_seq_len, a->split_size) > 65535)
     return fail(L20_PD_EINVAL, "batch and the split count must be at most 65535");
+  if ((int64_t)a->batch * a->q_len * a->num_q_heads > INT32_MAX)
+    return fail(L20_PD_EINVAL, "batch x q_len x Q heads must be below 2^31");
   if (a->batch == 0) return L20_PD_OK;
   if (!a->query || !a->key_cache || !a->value_cache || !a->block_table || !a->seq_lens || !a->output)
     return fail(L20_PD_EINVAL, "null tensor pointer");
@@ -1781,8 +1797,18 @@ template <typename QT, int D, int WPP>
 hipError_t launch_merge_wpp(const l20pd::MergeParams &mp, int64_t pairs, hipStream_t stream) {
   constexpr int WPB = WPP > 4 ? WPP : 4;
   constexpr int PPB = WPB / WPP;
-  hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP>), dim3((unsigned)((pairs + PPB - 1) / PPB)), dim3(64 * WPB), 0,
-                     stream, mp);
+  const dim3 grid((unsigned)((pairs + PPB - 1) / PPB)), block(64 * WPB);
+  if (mp.po_kind == 0) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 0>), grid, block, 0, stream, mp);
+  else if (mp.po_kind == 1) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 1>), grid, block, 0, stream, mp);
+  else hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 2>), grid, block, 0, stream, mp);
+  return hipGetLastError();
+}
+
+template <typename QT, int D, int PK, int NSL>
+hipError_t launch_merge_narrow(const l20pd::MergeParams &mp, int64_t pairs, hipStream_t stream) {
+  constexpr int64_t per_block = 4 * (64 / (D / 8));  // 4 waves of 64 / (D/8) pairs
+  hipLaunchKernelGGL((l20pd::pd_merge_narrow<QT, D, PK, NSL>), dim3((unsigned)((pairs + per_block - 1) / per_block)),
+                     dim3(256), 0, stream, mp);
   return hipGetLastError();
 }
 
@@ -1804,10 +1830,18 @@ hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipSt
     // 7.4 us between the partial kernel and the end of the call): 64 / (D/8)
     // pairs per wave, 4 waves per workgroup, one round trip.  Few pairs keep one
     // wave per pair, which spreads a small merge over more waves.
-    const int64_t per_block = 4 * (64 / (D / 8));
-    hipLaunchKernelGGL((l20pd::pd_merge_narrow<QT, D>), dim3((unsigned)((pairs + per_block - 1) / per_block)), dim3(256),
-                       0, stream, mp);
-    return hipGetLastError();
+    const int nsl = mp.num_splits <= 2 ? 2 : mp.num_splits <= 4 ? 4 : 8;
+    switch (3 * (nsl == 2 ? 0 : nsl == 4 ? 1 : 2) + (mp.po_kind == 0 ? 0 : mp.po_kind == 1 ? 1 : 2)) {
+      case 0: return launch_merge_narrow<QT, D, 0, 2>(mp, pairs, stream);
+      case 1: return launch_merge_narrow<QT, D, 1, 2>(mp, pairs, stream);
+      case 2: return launch_merge_narrow<QT, D, 2, 2>(mp, pairs, stream);
+      case 3: return launch_merge_narrow<QT, D, 0, 4>(mp, pairs, stream);
+      case 4: return launch_merge_narrow<QT, D, 1, 4>(mp, pairs, stream);
+      case 5: return launch_merge_narrow<QT, D, 2, 4>(mp, pairs, stream);
+      case 6: return launch_merge_narrow<QT, D, 0, 8>(mp, pairs, stream);
+      case 7: return launch_merge_narrow<QT, D, 1, 8>(mp, pairs, stream);
+      default: return launch_merge_narrow<QT, D, 2, 8>(mp, pairs, stream);
+    }
   }
   switch (merge_waves_per_pair(mp.num_splits, D)) {
     case 1: return launch_merge_wpp<QT, D, 1>(mp, pairs, stream);

@@ -155,6 +155,17 @@ def test_check_rejects_bad_arguments(field, value, message):
     assert message in cabi.last_error(lib)
 
 
+def test_check_rejects_pair_count_beyond_int32():
+    # the merge kernels index (query row, q head) pairs in 32 bits
+    a = valid_args()
+    a.num_q_heads = a.num_kv_heads = 1 << 30
+    message = "batch x q_len x Q heads must be below 2^31"
+    with pytest.raises(RuntimeError, match=re.escape(message)):
+        cabi.check(a)
+    lib = cabi.load()
+    assert lib.l20_pd_fp8_e4m3_split_out(ctypes.byref(a), None) == cabi.L20_PD_EINVAL
+
+
 def test_single_split_needs_no_workspace():
     a = valid_args()
     a.max_seq_len, a.split_size = 200, 256
