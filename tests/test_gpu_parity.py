@@ -153,6 +153,9 @@ def test_merge_waves_per_pair(d, lens, split, pdt):
     (128, [4096, 4000, 1030, 5, 0], 1024, torch.float32),   # 4 slots, ragged rows
     (64, [511, 300, 64, 1], 64, torch.float16),              # 8 slots (the narrow limit), fp16 partials
     (128, [900, 2000], 256, torch.float32),                  # 8 slots, q_len 4 below
+    (128, [2048, 1500, 3, 0], 1024, torch.bfloat16),         # 2 slots, bf16 partials
+    (128, [1536, 700], 512, torch.float16),                  # 3 splits read as 4 slots (slot 3 rereads 0)
+    (64, [300, 129, 64], 64, torch.bfloat16),                # 5 splits read as 8 slots, bf16 partials
 ])
 @pytest.mark.parametrize("q_len", [1, 4])
 def test_narrow_merge_ignores_stale_slots(d, lens, split, pdt, q_len):
