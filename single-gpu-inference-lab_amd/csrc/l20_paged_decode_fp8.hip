@@ -17,9 +17,10 @@
 //      softmax: each lane holds 8 scores of one query column; the block max is
 //         reduced across the four 16-lane groups; exp2 with the K scale, the
 //         softmax scale and log2(e) folded into one multiplier.
-//      V: 8 tokens x D/16 contiguous bytes per lane; the fp8 -> f32 -> f16
-//         conversion packs token pairs, which transposes V for the MFMA A
-//         operand in registers (no LDS pass).  O^T += V^T . P^T with P in f16.
+//      V: 8 tokens x D/16 contiguous bytes per lane; a byte permute and the
+//         fp8 -> f16 conversion pack token pairs, which transposes V for the
+//         MFMA A operand in registers (no LDS pass).  O^T += V^T . P^T with P
+//         in f16.
 //    A sequence with a single split writes the final output and LSE;
 //    otherwise the fp32 partial (O / l, m, l) goes to the caller's workspace.
 //
@@ -640,7 +641,13 @@ struct KvUnit {
     for (int tp2 = 0; tp2 < NT; tp2 += 2) {
       i32x4 wa, wb;
       if constexpr (KT != 1) {
-        // d tiles tp2, tp2+1 use byte pair (tp2 % 4, tp2 % 4 + 1) of dword tp2 / 4
+        // d tiles tp2, tp2+1 use byte pair (c, c + 1), c = tp2 % 4, of dword tp2 / 4.
+        // One byte permute interleaves tokens e and e + 1 (bytes w0.c, w1.c,
+        // w0.c+1, w1.c+1), and each half of the result converts straight to an
+        // f16 pair (token e, token e + 1) of one dim: 3 VALU instructions per
+        // four elements, against 4 through fp32.  v_perm_b32 selectors 0-3 pick
+        // bytes of its second operand, 4-7 of its first.
+        const uint32_t sel = (tp2 & 3) ? 0x03070206u : 0x01050004u;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
           int w0, w1;
@@ -651,10 +658,9 @@ struct KvUnit {
             w0 = r.v[e];
             w1 = r.v[e + 1];
           }
-          const f32x2 f0 = fp8x2_f32<KT == 2>(w0, (tp2 & 3) != 0);
-          const f32x2 f1 = fp8x2_f32<KT == 2>(w1, (tp2 & 3) != 0);
-          wa[e >> 1] = pack2<_Float16>(f0[0], f1[0]);
-          wb[e >> 1] = pack2<_Float16>(f0[1], f1[1]);
+          const int x = (int)__builtin_amdgcn_perm((uint32_t)w0, (uint32_t)w1, sel);
+          wa[e >> 1] = cvt_pk_f16<KT == 2>(x, false);
+          wb[e >> 1] = cvt_pk_f16<KT == 2>(x, true);
         }
       } else {
         // d tiles tp2, tp2+1 are the low and high halves of dword tp2 / 2:
