@@ -178,6 +178,23 @@ __device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, f32x4 c)
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Empty asm statements that take a value in VGPRs: the loads producing it
+// complete at this point instead of at its first use.
+template <typename V8, int A, int B> __device__ __forceinline__ void pin_operands(V8 (&x)[A][B]) {
+#pragma unroll
+  for (int a = 0; a < A; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      i32x4 w = __builtin_bit_cast(i32x4, x[a][b]);
+      asm volatile("" : "+v"(w));
+      x[a][b] = __builtin_bit_cast(V8, w);
+    }
+}
+template <int N> __device__ __forceinline__ void pin_words(int (&x)[N]) {
+#pragma unroll
+  for (int a = 0; a < N; ++a) asm volatile("" : "+v"(x[a]));
+}
+
 // Byte pair (sel=0: bytes 0,1; sel=1: bytes 2,3) of a dword -> two f32.
 template <bool E5M2> __device__ __forceinline__ f32x2 fp8x2_f32(int w, bool hi) {
   if constexpr (E5M2)
@@ -338,17 +355,19 @@ struct KvUnit {
   static constexpr int NS = 2 * NCH;  // 32-wide k slices of the QK product
   static constexpr int NT = D / 16;   // 16-row d tiles of the PV product
   static constexpr int DPL = D / 4;   // contiguous output dims per lane
-  // KLINES (fp8 K at head_dim 128, one block in flight): K arrives in whole
+  // KLINES (fp8 K at head_dim 128; not for two query tiles with two blocks
+  // in flight, which would spill more): K arrives in whole
   // 128-byte lines (lane l: token 8c + l/8 of page T, bytes 16 (l % 8)) and
   // goes through the wave's own LDS rows into the MFMA layout (lane (n16, j):
   // token n16, bytes 16 j + 64 c).  Loading the MFMA layout straight from
   // memory takes half of 16 lines per instruction; in load-only kernels over
   // the config-3 pages and schedule that streamed at 4.7 TB/s against 5.6 for
   // whole lines.  In the full kernels the pass gains 1.6 us at config 4 (85.4
-  // vs 87.1 us, same box) and nothing at config 5, both one block in flight,
-  // but costs 1.1 us in the two-block kernel of config 3 (10 more VGPRs), which
-  // keeps the direct loads.  Rows are padded to 144 bytes so that the 16 rows
-  // of a read fall in distinct banks.
+  // vs 87.1 us, same box) and nothing at config 5, both one block in flight;
+  // in the two-block kernel of config 3 it gains 1.4 us once that kernel's
+  // loads are issued in the same order on every path (it cost 1.1 us while the
+  // compiler drained the stream before every other block).  Rows are padded
+  // to 144 bytes so that the 16 rows of a read fall in distinct banks.
   static constexpr bool kKLines = KLINES;
   static constexpr int kKxRow = 144;                  // LDS bytes per token row
   static constexpr int kKxBytes = 2 * 16 * kKxRow;    // two pages per block
@@ -370,21 +389,39 @@ struct KvUnit {
   // Raw buffer loads through a per-page resource: the page base lives in
   // SGPRs, one 32-bit lane offset serves every K (V) load of the page and the
   // hardware range check (the page's byte extent) returns zeros for anything
-  // outside it.  Loads are unconditional -- an invalid page id reads page 0 --
-  // and compute_block zeroes V of every token outside the unit or on an
-  // invalid page.  Lane offsets inside a page fit in 32 bits (checked on the
+  // outside it.  Loads are unconditional -- an invalid page id, or none, reads
+  // zeros through a zero-extent resource -- and compute_block masks every
+  // token outside the unit or on an invalid page and zeroes its V.  Lane offsets inside a page fit in 32 bits (checked on the
   // host).  parts: 1 = the K loads, 2 = the V loads, 3 = both.
+  static constexpr int kPagesPerBlock = KT == 1 ? 1 : 2;
+  // Page ids of block blk of a unit (lane t of pid holds tile t's id, -1 for
+  // none), wave-uniform.
+  static __device__ __forceinline__ void block_pages(int pid, int blk, int (&pg)[2]) {
+#pragma unroll
+    for (int T = 0; T < 2; ++T) pg[T] = T < kPagesPerBlock ? __builtin_amdgcn_readlane(pid, kPagesPerBlock * blk + T) : -1;
+  }
   static __device__ __forceinline__ void load_block(const PartialParams &p, Block &r, int pid, int kvh, int blk,
+                                                    int parts, int n16, int j) {
+    int pg[2];
+    block_pages(pid, blk, pg);
+    load_pages(p, r, pg, kvh, parts, n16, j);
+  }
+  // The loads of one block from its pages: straight-line code, no branch
+  // around any load, K of every page before V of every page (a refill issued
+  // in two parts keeps the same order).  A page id below 0 (none, or an
+  // invalid one) gets a resource of zero extent: its loads return zeros
+  // without touching memory, and compute_block masks those tokens.
+  static __device__ __forceinline__ void load_pages(const PartialParams &p, Block &r, const int (&pg)[2], int kvh,
                                                     int parts, int n16, int j) {
     if constexpr (KT == 1) {
       // 16-bit elements: one page per block; K slice s at byte 128*(s/2) + 16*(s%2)
       const uint32_t koff = (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 32 * j);
       const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + 2 * (D / 16) * n16);
-      const int raw_page = __builtin_amdgcn_readlane(pid, blk);
-      const int page = raw_page >= 0 ? raw_page : 0;
+      const int page = max(pg[0], 0);
+      const bool live = pg[0] >= 0;
       if (parts & 1) {
         const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+            const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, live ? p.k_extent : 0, kBufferWord3);
 #pragma unroll
         for (int s = 0; s < NS; ++s)
           r.k[s] = __builtin_bit_cast(
@@ -392,7 +429,7 @@ struct KvUnit {
       }
       if (parts & 2) {
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+            const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, live ? p.v_extent : 0, kBufferWord3);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if constexpr (D == 128)
@@ -407,22 +444,25 @@ struct KvUnit {
       const uint32_t koff = kKLines ? (uint32_t)((lane >> 3) * p.k_stok32 + kvh * p.k_shead32 + 16 * (lane & 7))
                                     : (uint32_t)(n16 * p.k_stok32 + kvh * p.k_shead32 + 16 * j);
       const uint32_t voff = (uint32_t)(4 * j * p.v_stok32 + kvh * p.v_shead32 + (D / 16) * n16);
+      if (parts & 1) {
 #pragma unroll
-      for (int T = 0; T < 2; ++T) {
-        const int raw_page = __builtin_amdgcn_readlane(pid, 2 * blk + T);
-        const int page = raw_page >= 0 ? raw_page : 0;
-        if (parts & 1) {
-          const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-              const_cast<uint8_t *>(p.k) + (int64_t)page * p.k_spage, (short)0, p.k_extent, kBufferWord3);
+        for (int T = 0; T < 2; ++T) {
+          const __amdgpu_buffer_rsrc_t kr =
+              __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.k) + (int64_t)max(pg[T], 0) * p.k_spage,
+                                                (short)0, pg[T] >= 0 ? p.k_extent : 0, kBufferWord3);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
             r.k[T][c] = __builtin_bit_cast(
                 i32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, kKLines ? 8 * c * p.k_stok32 : 64 * c,
                                                              kStreamPolicy));
         }
-        if (parts & 2) {
-          const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-              const_cast<uint8_t *>(p.v) + (int64_t)page * p.v_spage, (short)0, p.v_extent, kBufferWord3);
+      }
+      if (parts & 2) {
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+          const __amdgpu_buffer_rsrc_t vr =
+              __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.v) + (int64_t)max(pg[T], 0) * p.v_spage,
+                                                (short)0, pg[T] >= 0 ? p.v_extent : 0, kBufferWord3);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             if constexpr (D == 128)
@@ -811,7 +851,7 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // fp32 partial (o / l, m, l) at its split slot.
 template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
-  typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128 && NB == 1> U;
+  typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128> U;
   typedef typename U::qvec8 qvec8;
   typedef typename U::Block Block;
   constexpr int kTok = U::kTok;            // tokens per block
@@ -892,6 +932,9 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   auto load_block = [&](Block &r, int pid, int kvh, int blk, int parts = 3) {
     U::load_block(p, r, pid, kvh, blk, parts, n16, j);
   };
+  auto load_pages = [&](Block &r, const int (&pg)[2], int kvh, int parts = 3) {
+    U::load_pages(p, r, pg, kvh, parts, n16, j);
+  };
 
   // ---- stream state (wave-uniform except the VGPR operands) ----
   Block buf[NB];
@@ -911,8 +954,15 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   if ((int)blockIdx.x >= G1) {
     cb = -2;  // starts on queue item blockIdx.x - G1
   } else {
-    // Page ids and the length leave together; the ids are masked to the
-    // split once the length is known.
+    // The query and tree words leave with the page ids and the length, before
+    // any K/V load: the wait for the ids covers them, so no step waits on a
+    // query load issued behind the stream.  (Issued after the first blocks'
+    // K/V, they were the most recent loads when the block loop began, and the
+    // loop's static wait before the score product drained every load in flight
+    // on each of its iterations.)  The ids are masked to the split once the
+    // length is known.
+    load_q(cb, wave, qop);
+    load_tree(cb, treeU);
     const int start = cs * S;
     const int spec = min(S / kPage, pages_of(cb) - start / kPage);
     int v = -1;
@@ -922,12 +972,12 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       const int tiles = max(0, (min(start + S, cL) - start + kPage - 1) / kPage);
       pidU = (lane < tiles && lane < spec && v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
       const int nU = KT != 1 ? (tiles + 1) >> 1 : tiles;
-      if (nU > 0) load_block(buf[0], pidU, wave, 0);
-      if constexpr (NB > 1)
-        if (nU > 1) load_block(buf[NB - 1], pidU, wave, 1);
+      // Both buffers load, a block past the unit's end reading page 0 (its
+      // tiles hold page id -1), so the stream enters its loop with the loads
+      // in flight of any later step.
+      load_block(buf[0], pidU, wave, 0);
+      if constexpr (NB > 1) load_block(buf[NB - 1], pidU, wave, 1);
       issuedU = min(nU, NB);
-      load_q(cb, wave, qop);
-      load_tree(cb, treeU);
       u_loaded = true;
     } else {
       cb = -2;  // hole: the workgroup starts on the queue
@@ -1162,19 +1212,28 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         load_tree(b, treeU);
         issuedU = 0;
       }
-      // top up the unit's first two blocks
+      // Top up the unit's first NB blocks (a block past the unit's end reads
+      // page 0: its tiles hold page id -1), so every path issues the same loads.
+      auto top_up = [&](Block &r, int blk) { load_block(r, pidU, kvh, blk); };
       if constexpr (NB == 1) {
-        if (issuedU < 1 && nU > 0) load_block(buf[0], pidU, kvh, 0);
+        if (issuedU < 1) top_up(buf[0], 0);
       } else {
-        if (issuedU < 1 && nU > 0) {
-          if (par) load_block(buf[NB - 1], pidU, kvh, 0);
-          else load_block(buf[0], pidU, kvh, 0);
+        if (issuedU < 1) {
+          if (par) top_up(buf[NB - 1], 0);
+          else top_up(buf[0], 0);
         }
-        if (issuedU < 2 && nU > 1) {
-          if (par) load_block(buf[0], pidU, kvh, 1);
-          else load_block(buf[NB - 1], pidU, kvh, 1);
+        if (issuedU < 2) {
+          if (par) top_up(buf[0], 1);
+          else top_up(buf[NB - 1], 1);
         }
       }
+      // The query (and tree words) must have arrived before the block loop:
+      // left pending, their loads sit behind the stream's on some path into
+      // the loop, and its static waits before the score product then drain
+      // every load in flight on each iteration.  The pin waits for them here,
+      // with the first blocks' K/V still in flight.
+      pin_operands(qop);
+      if constexpr (TREE) pin_words(treeU);
 
       // ---- the next unit of this wave ----
       bool hasN = false;
@@ -1248,19 +1307,27 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         const int pos = k + NB;
         const bool own = pos < nU;
         const bool nxt = !own && pos - nU == issuedN && issuedN < nN;
+        // Every step issues its refill's loads -- a dummy block reading page 0
+        // when the stream has nothing left -- from one straight-line sequence:
+        // only the page ids are chosen per case.  With the same loads, in the
+        // same order, on every path the compiler's load counters wait for r's
+        // block alone; refills issued on some paths and not others (or
+        // partly merged across the cases) made it wait for every load in
+        // flight, the other buffer's refill included, before the next block.
+        int pg[2] = {-1, -1};
+        int rkvh = kvh;
+        if (own) {
+          U::block_pages(pidU, pos, pg);
+        } else if (nxt) {
+          U::block_pages(pidN, issuedN, pg);
+          rkvh = nKvh;
+        }
         compute_block(r, k, [&]() {
-          if constexpr (NB > 1) {
-            if (own) load_block(r, pidU, kvh, pos, 1);
-            else if (nxt) load_block(r, pidN, nKvh, issuedN, 1);
-          }
+          if constexpr (NB > 1) load_pages(r, pg, rkvh, 1);
         });
         constexpr int kLate = NB > 1 ? 2 : 3;  // the parts left for after the block
-        if (own) {
-          load_block(r, pidU, kvh, pos, kLate);
-        } else if (nxt) {
-          load_block(r, pidN, nKvh, issuedN, kLate);
-          ++issuedN;
-        }
+        load_pages(r, pg, rkvh, kLate);
+        if (nxt) ++issuedN;
         if (k == k_claim) claim_point();
         // From the checkpoint on, poll for the successor; wait for it
         // kNeedLead blocks before the end (its first block is the refill
