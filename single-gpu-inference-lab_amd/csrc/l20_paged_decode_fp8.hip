@@ -851,7 +851,7 @@ __device__ __forceinline__ int static_splits(int b, int G, int B) { return b < G
 // fp32 partial (o / l, m, l) at its split slot.
 template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
-  typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128> U;
+  typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128 && (NB == 1 || NQT == 1)> U;
   typedef typename U::qvec8 qvec8;
   typedef typename U::Block Block;
   constexpr int kTok = U::kTok;            // tokens per block
