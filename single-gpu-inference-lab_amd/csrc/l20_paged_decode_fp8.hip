@@ -207,15 +207,35 @@ template <typename QT> __device__ __forceinline__ QT from_f32(float x);
 template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
 template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
 
+// Reductions over lanes l, l^16, l^32 and l^48 done in VGPRs, not through
+// LDS: with both operands the same register, v_permlane16_swap returns per
+// lane the values of the even and the odd 16-lane row of its row pair, and
+// v_permlane32_swap those of the two 32-lane halves, so combining the two
+// results gives every lane the pair (l, l^16), then (l, l^32).  Both lanes of
+// a pair combine the same two operands (fmax and + commute exactly), so all
+// four lanes end with the same bits.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+template <int W> __device__ __forceinline__ u32x2_t swap_rows(float x) {
+  const unsigned int b = __builtin_bit_cast(unsigned int, x);
+  if constexpr (W == 16) return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_permlane16_swap(b, b, false, false));
+  else return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_permlane32_swap(b, b, false, false));
+}
+// The element is taken by value: hipcc lowers __builtin_bit_cast of an
+// ext_vector element expression (v[1]) to a load of element 0.
+__device__ __forceinline__ float word_f(unsigned int w) { return __builtin_bit_cast(float, w); }
+__device__ __forceinline__ float lo_f(u32x2_t v) { return word_f(v[0]); }
+__device__ __forceinline__ float hi_f(u32x2_t v) { return word_f(v[1]); }
 __device__ __forceinline__ float wave_max_xor16_32(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  u32x2_t r = swap_rows<16>(x);
+  x = fmaxf(lo_f(r), hi_f(r));
+  r = swap_rows<32>(x);
+  return fmaxf(lo_f(r), hi_f(r));
 }
 __device__ __forceinline__ float wave_sum_xor16_32(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  u32x2_t r = swap_rows<16>(x);
+  x = lo_f(r) + hi_f(r);
+  r = swap_rows<32>(x);
+  return lo_f(r) + hi_f(r);
 }
 
 // Raw fp8 bytes of one 32-token block (two 16-token pages) held by one lane.
