@@ -85,3 +85,72 @@ def test_probability_rounding_does_not_bias_long_contexts(kv, split):
     err = float(np.abs(out.float().cpu().numpy() - exact).max())
     assert err < 3.9e-3, err
     assert float(np.abs(lse.cpu().numpy() - exact_lse).max()) < 1e-5 * exact_lse
+
+
+SPIKE_L = 600      # 19 blocks of 32 tokens, two 512-token splits
+SPIKE_B = 32       # one sequence per token position inside a 32-token block
+
+
+def spiky(kv: str, q_len: int):
+    """Sequence b holds one spike key at position b of every 32-token block.
+
+    The spike keys score ~30 log2 units above the rest (key 16.0 against keys
+    in [-1, 1] along the query's one non-zero dimension), so a block's maximum
+    sits in whichever lane row holds position b.  A maximum reduced over only
+    some lane rows leaves the spikes' probabilities at ~2^30, far past f16's
+    range, and the output turns inf/NaN; the exact maximum gives the mean of
+    the spikes' values.
+    """
+    g = torch.Generator().manual_seed(11)
+    per = (SPIKE_L + 15) // 16
+    pages = SPIKE_B * per
+    perm = torch.randperm(pages + 5, generator=g)[:pages].to(torch.int32)
+    table = perm.view(SPIKE_B, per)
+    key = torch.zeros(pages + 5, 16, HKV, D)
+    val = torch.zeros(pages + 5, 16, HKV, D)
+    tok = torch.arange(SPIKE_L)
+    for b in range(SPIKE_B):
+        slots = table[b].long().repeat_interleave(16)[:SPIKE_L] * 16 + tok % 16
+        k0 = torch.rand(SPIKE_L, generator=g) * 2.0 - 1.0
+        k0[tok % 32 == b] = 16.0
+        key.view(-1, HKV, D)[slots, 0, 0] = k0
+        val.view(-1, HKV, D)[slots, 0, :] = torch.rand(SPIKE_L, D, generator=g) * 8.0 - 4.0
+    query = torch.zeros(SPIKE_B * q_len, HQ, D)
+    query[:, :, 0] = 16.0
+    inp = {
+        "query": query.to(torch.float16).cuda(), "block_table": table.cuda(),
+        "seq_lens": torch.full((SPIKE_B,), SPIKE_L, dtype=torch.int32).cuda(), "softmax_scale": D ** -0.5,
+        "q_len": q_len, "max_seq_len": SPIKE_L,
+    }
+    if kv == "fp8":
+        inp.update(key_cache=key.to(torch.float8_e4m3fn).cuda(), value_cache=val.to(torch.float8_e4m3fn).cuda(),
+                   k_scale=1.0, v_scale=1.0)
+    else:
+        inp.update(key_cache=key.to(torch.float16).cuda(), value_cache=val.to(torch.float16).cuda())
+    return inp
+
+
+@pytest.mark.parametrize("kv", ["fp8", "fp16"])
+@pytest.mark.parametrize("q_len", [1, 4])
+@pytest.mark.parametrize("split", [256, 512])
+def test_block_maximum_covers_every_lane_row(kv, q_len, split):
+    inp = spiky(kv, q_len)
+    if kv == "fp8":
+        out, lse = H.run_op(inp, split)
+        exp_out, exp_lse = H.run_oracle(inp)
+    else:
+        out, lse = H.run_op16(inp, split)
+        exp_out, exp_lse = H.run_oracle16(inp)
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(lse).all())
+    H.compare(out, lse, exp_out, exp_lse)
+    # Closed form: the other keys weigh < 600 * 2^-28 against a spike, so each
+    # query row's output is the mean of the values of the spikes it can see.
+    vc = inp["value_cache"].float().cpu().view(-1, HKV, D)
+    table = inp["block_table"].cpu().long()
+    got = out.float().cpu().view(SPIKE_B, q_len, HQ, D)
+    for b in range(SPIKE_B):
+        for i in range(q_len):
+            seen = torch.arange(b, SPIKE_L - q_len + i + 1, 32)
+            spikes = vc[table[b, seen // 16] * 16 + seen % 16, 0]
+            err = float((got[b, i] - spikes.mean(0)).abs().max())
+            assert err < 2e-2, (b, i, err)
