@@ -269,6 +269,17 @@ template <int D> struct KvBlock<1, D> { typedef BlockRaw16<D> type; };
 // Partial kernel
 // ---------------------------------------------------------------------------
 // Two fp32 -> packed 16-bit words (bf16 or f16, round to nearest even).
+// p - (float)h, h the low (HI = 0) or high f16 half of w, in one VOP3P mix
+// instruction: the f16 operand widens exactly and the f32 result is rounded
+// once (p - h is exact anyway).  hipcc forms no mix instruction from
+// fmaf((float)h, -1, p), hence the inline assembly.
+template <int HI> __device__ __forceinline__ float sub_half(int w, float p) {
+  float r;
+  if constexpr (HI) asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(p));
+  else asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(p));
+  return r;
+}
+
 template <typename QT> __device__ __forceinline__ int pack2(float a, float b);
 template <> __device__ __forceinline__ int pack2<__bf16>(float a, float b) {
   return __builtin_bit_cast(int, __builtin_convertvector(f32x2{a, b}, bf16x2));
@@ -682,10 +693,10 @@ struct KvUnit {
             pw_lo[e >> 1] =
                 pack2<PT>(p0 - __builtin_bit_cast(float, w << 16), p1 - __builtin_bit_cast(float, w & 0xffff0000u));
           } else {
-            // f16 round trips of p0 and p1 themselves (the same RNE rounding as
-            // the packed word): ROCm 7.2's LLVM folds element extraction from
-            // the packed words of this loop into the first pair's halves.
-            pw_lo[e >> 1] = pack2<PT>(p0 - (float)(_Float16)p0, p1 - (float)(_Float16)p1);
+            // p - hi straight from the packed word's halves: one mix
+            // instruction per element instead of a widening and a subtraction.
+            const int h = pw[e >> 1];
+            pw_lo[e >> 1] = pack2<PT>(sub_half<0>(h, p0), sub_half<1>(h, p1));
           }
         }
       }
