@@ -765,10 +765,30 @@ struct KvUnit {
   // LSE (and, with a workspace, mark split slot 0 of the row +inf for the
   // merge).  Otherwise write the fp32 (or fp16) partial (O / l, m, l) of query
   // row i at workspace row slot_row * q_len + i, split slot_split.
+  // KERNARG: read the output pointers and strides at the epilogue from the
+  // kernel's argument segment (the partial kernel's only argument) instead of
+  // keeping them in scalar registers across the block loop.  With one block
+  // in flight this halves the scalar spills into VGPR lanes and their reloads
+  // in every block (long units: config 4 84.8 -> 83.7 us); with two blocks the
+  // epilogue's extra scalar round trip costs more on the short units it
+  // serves (config 3 +0.5 us), so those kernels keep the registers.
+  template <bool KERNARG>
   __device__ __forceinline__ void finish(const PartialParams &p, int b, int kvh, bool direct, int64_t slot_row,
                                          int64_t slot_split, bool mark_final, float v_scale, int n16, int j) {
-    const int q_len = p.q_len;
-    const int mcols = p.group * q_len;
+    if constexpr (KERNARG) {
+      typedef const __attribute__((address_space(4))) PartialParams *KernargParams;
+      KernargParams kp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(kp));  // no reuse of values loaded before this point
+      finish_with(kp, b, kvh, direct, slot_row, slot_split, mark_final, v_scale, n16, j);
+    } else {
+      finish_with(&p, b, kvh, direct, slot_row, slot_split, mark_final, v_scale, n16, j);
+    }
+  }
+  template <typename PP>
+  __device__ __forceinline__ void finish_with(PP pp, int b, int kvh, bool direct, int64_t slot_row,
+                                              int64_t slot_split, bool mark_final, float v_scale, int n16, int j) {
+    const int q_len = pp->q_len;
+    const int mcols = pp->group * q_len;
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
       const float l_tot = wave_sum_xor16_32(l_run[qt]);
@@ -777,10 +797,10 @@ struct KvUnit {
       const float inv = (l_tot > 0.0f) ? v_scale / l_tot : 0.0f;
       const int g = col / q_len;
       const int i = col - g * q_len;
-      const int64_t h = (int64_t)kvh * p.group + g;
+      const int64_t h = (int64_t)kvh * pp->group + g;
       if (direct) {
         const int64_t row = (int64_t)b * q_len + i;
-        QT *dst = reinterpret_cast<QT *>(p.out) + row * p.o_srow + h * p.o_shead + DPL * j;
+        QT *dst = reinterpret_cast<QT *>(pp->out) + row * pp->o_srow + h * pp->o_shead + DPL * j;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           if constexpr (D == 128) {
@@ -795,27 +815,27 @@ struct KvUnit {
             *reinterpret_cast<i32x2 *>(dst + rr * NT) = w;
           }
         }
-        if (j == 0 && p.lse) {
+        if (j == 0 && pp->lse) {
           const float m = (m_run[qt] == -INFINITY) ? 0.0f : m_run[qt];
           // v_log_f32 is log2
-          p.lse[row * p.lse_srow + h * p.lse_shead] = (l_tot > 0.0f) ? kLn2 * (m + __builtin_amdgcn_logf(l_tot)) : -INFINITY;
+          pp->lse[row * pp->lse_srow + h * pp->lse_shead] = (l_tot > 0.0f) ? kLn2 * (m + __builtin_amdgcn_logf(l_tot)) : -INFINITY;
         }
-        if (j == 0 && mark_final) p.pm[row * p.pm_srow + h * p.pm_shead] = INFINITY;  // merge: already final
+        if (j == 0 && mark_final) pp->pm[row * pp->pm_srow + h * pp->pm_shead] = INFINITY;  // merge: already final
       } else {
         const int64_t prow = slot_row * q_len + i;
-        const int64_t po_idx = prow * p.po_srow + h * p.po_shead + slot_split * p.po_ssplit + DPL * j;
+        const int64_t po_idx = prow * pp->po_srow + h * pp->po_shead + slot_split * pp->po_ssplit + DPL * j;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          if (p.po_kind == 0) {
-            float *dst = reinterpret_cast<float *>(p.po) + po_idx + rr * NT;
+          if (pp->po_kind == 0) {
+            float *dst = reinterpret_cast<float *>(pp->po) + po_idx + rr * NT;
 #pragma unroll
             for (int t = 0; t < NT; t += 4)
               *reinterpret_cast<f32x4 *>(dst + t) = f32x4{acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv,
                                                           acc[qt][t + 2][rr] * inv, acc[qt][t + 3][rr] * inv};
           } else {
             // 16-bit partials: 2 bytes per element at the same element offsets
-            _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx + rr * NT;
-            const bool bf = p.po_kind == 2;
+            _Float16 *dst = reinterpret_cast<_Float16 *>(pp->po) + po_idx + rr * NT;
+            const bool bf = pp->po_kind == 2;
             if constexpr (D == 128) {
               i32x4 w;
 #pragma unroll
@@ -834,8 +854,8 @@ struct KvUnit {
           }
         }
         if (j == 0) {
-          p.pm[prow * p.pm_srow + h * p.pm_shead + slot_split * p.pm_ssplit] = m_run[qt];
-          p.pl[prow * p.pl_srow + h * p.pl_shead + slot_split * p.pl_ssplit] = l_tot;
+          pp->pm[prow * pp->pm_srow + h * pp->pm_shead + slot_split * pp->pm_ssplit] = m_run[qt];
+          pp->pl[prow * pp->pl_srow + h * pp->pl_shead + slot_split * pp->pl_ssplit] = l_tot;
         }
       }
     }
@@ -1389,7 +1409,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         }
 
       // ---- epilogue ----
-      st.finish(p, b, kvh, direct, b, split, direct && has_ws, v_scale, n16, j);
+      st.template finish<NB == 1>(p, b, kvh, direct, b, split, direct && has_ws, v_scale, n16, j);
 
       // ---- the next unit inherits the stream ----
       par = (par + nU) % NB;
