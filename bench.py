@@ -68,8 +68,9 @@ def parse():
     ap.add_argument("--hot", action="store_true", help="reuse one input set (cache-warm, informational)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--partial-dtype", choices=["fp32", "fp16"], default="fp32",
-                    help="split-partial workspace dtype (the op accepts both; fp32 is the default)")
+    ap.add_argument("--partial-dtype", choices=["fp32", "fp16"], default="fp16",
+                    help="split-partial workspace dtype (the op accepts both; fp16 is the reference "
+                         "op's own: half* partial_output, l20_paged_decode.cu:162,297)")
     ap.add_argument("--cpu-sample", type=int, default=0, help="sequences (tokens for kv_write) in the CPU sample")
     ap.add_argument("--settle-ms", type=float, default=250.0,
                     help="untimed calls before the warmup steps, until this much wall time has passed")

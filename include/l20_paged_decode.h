@@ -163,7 +163,11 @@ int32_t l20_pd_fp8_e4m3_check(const l20_pd_fp8_args *args);
  * calls on one stream run in order and share its slot, up to 48 streams get
  * slots of their own (least recently used ones are shared beyond that), and a
  * call captured into a HIP graph takes one of 16 further slots in turn, since
- * the graph may replay on any stream.
+ * the graph may replay on any stream.  Two launches that overlap in time on
+ * one slot (a 49th stream in use at once, one graph replayed on two streams
+ * at once, or two graphs captured 16 captures apart replayed at once) are
+ * reported through l20_pd_device_errors (L20_PD_DEVERR_QUEUE_SHARED) whenever
+ * their claims interleave; a launch that claims nothing shares nothing.
  * (<- l20_paged_decode_fp8_e4m3_split_out_cuda, l20_paged_decode.cu:651-725) */
 int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
 
@@ -174,17 +178,27 @@ int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *args, void *stream);
  * then incomplete).  Returns the bitwise OR of the codes recorded on the
  * current device since the last clear (0: none), or -L20_PD_ELAUNCH on a HIP
  * error.  Synchronizes the device.  clear != 0 zeroes the error words and
- * the work-queue counters of the slots that had one; call it only while no
- * call of this library is in flight. */
+ * the work-queue counters of every slot; call it only while no call of this
+ * library is in flight. */
 #define L20_PD_DEVERR_PREFIX_WAIT 1   /* the per-sequence item table was never published */
 #define L20_PD_DEVERR_ACK_WAIT 2      /* a wave never acknowledged the published item */
 #define L20_PD_DEVERR_PUBLISH_WAIT 4  /* the next item was never published */
+#define L20_PD_DEVERR_QUEUE_SHARED 32 /* a work-queue claim found the counter in use by
+                                         another launch: two launches overlapped on one
+                                         slot (see l20_pd_fp8_e4m3_split_out), or one that
+                                         gave up left it mid-way.  The workgroup stops
+                                         claiming, so this launch's results (and the
+                                         other's) may be incomplete, and the slot stays
+                                         flagged until cleared: synchronize, clear, and
+                                         repeat the calls */
 int32_t l20_pd_device_errors(int32_t clear);
 
-/* Polls before a hand-off wait gives up, on the current device (0 restores
- * the default, ~0.1 s of polling).  A test hook with no reference
- * counterpart: a limit of 1 makes the waits give up at once, which exercises
- * the give-up path while every kernel still exits normally.  Synchronous. */
+/* Polls before a hand-off wait gives up, for calls enqueued on the current
+ * device after this one (0 restores the default, ~0.1 s of polling; a call
+ * captured into a graph keeps the limit it was captured with).  A test hook
+ * with no reference counterpart: a limit of 1 makes the waits give up at
+ * once, which exercises the give-up path while every kernel still exits
+ * normally. */
 int32_t l20_pd_set_spin_limit(uint32_t polls);
 
 /* Allocation-free variant of l20_pd_fp8_e4m3_split_out (no counterpart in the

@@ -46,7 +46,6 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
-#include <vector>
 #include <type_traits>
 
 #include "l20_paged_decode.h"
@@ -118,6 +117,15 @@ struct PartialParams {
   const int32_t *tree;    // ancestor words [b * tree_sb + i] (bit j: row i sees draft key j), or NULL
   int64_t tree_sb;
   int queue_slot;  // the launch's work-queue counters (g_pd_queue row)
+  // Two items per workgroup (kernels that support it): waves [0, W) and
+  // [W, 2W) are two independent groups, virtual workgroups blockIdx.x and
+  // gridDim.x + blockIdx.x of the schedule.
+  int paired;
+  // Polls before a hand-off wait gives up: kSpinLimit unless lowered through
+  // l20_pd_set_spin_limit (tests force the give-up path with it).
+  unsigned int spin_cap;
+  // Host launch number, mixed into the launch's work-queue tag.
+  unsigned int launch_tag;
 };
 
 // ---------------------------------------------------------------------------
@@ -330,22 +338,57 @@ __device__ __forceinline__ int lds_poll(int *a) { return __hip_atomic_load(a, __
 __device__ __forceinline__ void lds_put(int *a, int v) {
   __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+// Release store / acquire load at workgroup scope: the publication of a
+// word that other waves poll, and the poll that reads it (every LDS access
+// of the publisher before the store is visible to a wave whose acquire load
+// returns the stored value).
+#ifndef L20_PD_LDS_ORDER
+#define L20_PD_LDS_ORDER 1
+#endif
+__device__ __forceinline__ void lds_publish(int *a, int v) {
+#if L20_PD_LDS_ORDER
+  __hip_atomic_store(a, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+#else
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#endif
+}
+__device__ __forceinline__ int lds_acquire(int *a) {
+#if L20_PD_LDS_ORDER
+  return __hip_atomic_load(a, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+#else
+  const int v = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return v;
+#endif
+}
+#if L20_PD_LDS_ORDER
+#define L20_PD_LDS_REL __ATOMIC_RELEASE
+#else
+#define L20_PD_LDS_REL __ATOMIC_RELAXED
+#endif
 
 __device__ __forceinline__ int splits_of_len(int len, int split) { return len > 0 ? (len + split - 1) / split : 1; }
 // Work queues of the persistent partial kernel, one per launch slot (one
-// 64-byte line each; word 0 is the next queue item).  Zero at load.  A launch
-// whose grid covers every split-major slot claims nothing.  Otherwise every
-// workgroup claims until a claim fails (returns >= Q, the queue length), so
-// exactly gridDim.x claims fail and the one that returns Q + gridDim.x - 1 is
-// the last atomic on the counter in this launch: its workgroup resets the
+// 64-byte line each; its first 8 bytes are the counter).  Zero at load.  A
+// launch whose grid covers every split-major slot claims nothing.  Otherwise
+// every workgroup claims until a claim fails (returns >= Q, the queue length),
+// so exactly gridDim.x claims fail and the one that returns Q + gridDim.x - 1
+// is the last atomic on the counter in this launch: its workgroup resets the
 // counter, and every launch starts from zero without a memset (a captured
 // graph replays correctly).  Claims on one line are served one at a time
 // (~11 ns each on MI355X), which is why nothing else (such as a count of
-// finished workgroups) shares it.  The host gives consecutive launches
-// consecutive slots, so up to kQueueSlots launches may overlap on one device
-// (different streams).
+// finished workgroups) shares it.
+//
+// A claim adds 1 + (tag << 32), tag being the launch's own 32-bit tag (a
+// host launch number mixed with the address of the launch's dispatch
+// packet, so two replays of one graph differ too): after k claims of one
+// launch the counter holds k in its low half and k * tag in its high half.
+// A claim that returns any other pair came after a claim of another launch
+// (two launches overlapping on one slot) or after one that gave up mid-way:
+// the workgroup records L20_PD_DEVERR_QUEUE_SHARED and stops claiming.
 constexpr int kQueueSlots = 64;
-__device__ __align__(64) unsigned int g_pd_queue[kQueueSlots][16];
+__device__ __align__(64) unsigned long long g_pd_queue[kQueueSlots][8];
 // Hand-off waits give up after this many polls (s_sleep 1 each, ~0.1 s in
 // all; a wait that the protocol satisfies ends within microseconds).  A wave
 // that gives up ORs an L20_PD_DEVERR_* code into g_pd_error[slot], takes no
@@ -353,10 +396,6 @@ __device__ __align__(64) unsigned int g_pd_queue[kQueueSlots][16];
 // (l20_pd_device_errors) instead of a hung GPU.
 constexpr unsigned int kSpinLimit = 1u << 22;
 __device__ unsigned int g_pd_error[kQueueSlots];
-// Polls before a wait gives up: kSpinLimit unless lowered through
-// l20_pd_set_spin_limit (tests force the give-up path with it).  Read when a
-// wait starts, so the block stream holds no register for it.
-__device__ unsigned int g_pd_spin_limit = kSpinLimit;
 
 // ---------------------------------------------------------------------------
 // Per-unit math of the partial kernel
@@ -774,19 +813,94 @@ struct KvUnit {
   // serves (config 3 +0.5 us), so those kernels keep the registers.
   template <bool KERNARG>
   __device__ __forceinline__ void finish(const PartialParams &p, int b, int kvh, bool direct, int64_t slot_row,
-                                         int64_t slot_split, bool mark_final, float v_scale, int n16, int j) {
+                                         int64_t slot_split, bool mark_final, float v_scale, int n16, int j,
+                                         char *kx) {
     if constexpr (KERNARG) {
       typedef const __attribute__((address_space(4))) PartialParams *KernargParams;
       KernargParams kp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
       asm volatile("" : "+s"(kp));  // no reuse of values loaded before this point
-      finish_with(kp, b, kvh, direct, slot_row, slot_split, mark_final, v_scale, n16, j);
+      finish_with(kp, b, kvh, direct, slot_row, slot_split, mark_final, v_scale, n16, j, kx);
     } else {
-      finish_with(&p, b, kvh, direct, slot_row, slot_split, mark_final, v_scale, n16, j);
+      finish_with(&p, b, kvh, direct, slot_row, slot_split, mark_final, v_scale, n16, j, kx);
+    }
+  }
+  // Whole-line epilogue for fp32 partial rows (kKLines kernels, D = 128),
+  // through the wave's LDS rows kx.  Each lane holds 32 contiguous dims of
+  // one column; written straight out, every store instruction would put
+  // 16-byte pieces into ~28 different 128-byte lines.  Instead 8 columns at a
+  // time go to LDS as the 512-byte rows they form in memory (padded by 16
+  // bytes so that the columns written together fall in distinct banks), and
+  // are read back 16 bytes per lane in row order: every 8 consecutive lanes
+  // store one whole line.  The rows are the wave's own (its K pass of the
+  // next block writes them only after these reads, in program order).
+  template <typename PP>
+  __device__ __forceinline__ void finish_staged(PP pp, int64_t slot_row, int64_t slot_split, int kvh, float v_scale,
+                                                int n16, int j, char *kx) {
+    constexpr int kRow = 4 * D;       // bytes per fp32 row
+    constexpr int kRs = kRow + 16;    // LDS row stride
+    constexpr int kCols = 8;          // columns per pass (4608 bytes of rows)
+    const int q_len = pp->q_len;
+    const int mcols = pp->group * q_len;
+    const int lane = n16 + 16 * j;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const float l_tot = wave_sum_xor16_32(l_run[qt]);
+      const float inv = (l_tot > 0.0f) ? v_scale / l_tot : 0.0f;
+      const int col = 16 * qt + n16;
+      if (j == 0 && col < mcols) {
+        const int g = col / q_len;
+        const int i = col - g * q_len;
+        const int64_t h = (int64_t)kvh * pp->group + g;
+        const int64_t prow = slot_row * q_len + i;
+        pp->pm[prow * pp->pm_srow + h * pp->pm_shead + slot_split * pp->pm_ssplit] = m_run[qt];
+        pp->pl[prow * pp->pl_srow + h * pp->pl_shead + slot_split * pp->pl_ssplit] = l_tot;
+      }
+      const int ncols = min(16, mcols - 16 * qt);
+      for (int c0 = 0; c0 < ncols; c0 += kCols) {
+        if (n16 >= c0 && n16 < c0 + kCols && n16 < ncols) {
+          char *rowp = kx + (n16 - c0) * kRs;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+            for (int t = 0; t < NT; t += 4)
+              *reinterpret_cast<f32x4 *>(rowp + 4 * (DPL * j + rr * NT + t)) =
+                  f32x4{acc[qt][t][rr] * inv, acc[qt][t + 1][rr] * inv, acc[qt][t + 2][rr] * inv,
+                        acc[qt][t + 3][rr] * inv};
+          }
+        }
+        const int nbytes = min(kCols, ncols - c0) * kRow;
+        for (int o0 = 0; o0 < nbytes; o0 += 1024) {
+          const int o = o0 + 16 * lane;
+          if (o < nbytes) {
+            const int c = o / kRow;
+            const int w = o - c * kRow;
+            const i32x4 v = *reinterpret_cast<const i32x4 *>(kx + c * kRs + w);
+            const int gc = 16 * qt + c0 + c;
+            const int g = gc / q_len;
+            const int i = gc - g * q_len;
+            const int64_t h = (int64_t)kvh * pp->group + g;
+            char *dst = reinterpret_cast<char *>(pp->po) +
+                        ((slot_row * q_len + i) * pp->po_srow + h * pp->po_shead + slot_split * pp->po_ssplit) * 4;
+            *reinterpret_cast<i32x4 *>(dst + w) = v;
+          }
+        }
+      }
     }
   }
   template <typename PP>
   __device__ __forceinline__ void finish_with(PP pp, int b, int kvh, bool direct, int64_t slot_row,
-                                              int64_t slot_split, bool mark_final, float v_scale, int n16, int j) {
+                                              int64_t slot_split, bool mark_final, float v_scale, int n16, int j,
+                                              char *kx) {
+    // Whole-line stores through LDS rows pay for fp32 partials of two query
+    // tiles (config 5 partial kernel 99.8 -> 97.7 us); with one tile, or 16-bit
+    // rows, the direct column stores are as fast or faster (config 3: 46.7 vs
+    // 47.6 us with fp16 partials).
+    if constexpr (kKLines && D == 128 && NQT > 1) {
+      if (!direct && pp->po_kind == 0) {
+        finish_staged(pp, slot_row, slot_split, kvh, v_scale, n16, j, kx);
+        return;
+      }
+    }
     const int q_len = pp->q_len;
     const int mcols = pp->group * q_len;
 #pragma unroll
@@ -918,34 +1032,51 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   constexpr int kClaimLead = claim_lead(NB);
 
   extern __shared__ int s_dyn[];  // compact mode: s_prefix[B + 1], s_len[B]
-  __shared__ int s_pub[2][3];  // published item (b, s, L); b = -1: none
-  __shared__ int s_seq[2];     // item number of the slot's contents
-  __shared__ int s_ack[2];     // waves other than 0 that have read the slot
+  __shared__ int s_pub[2][2][3];  // per wave group: published item (b, s, L); b = -1: none
+  __shared__ int s_cap;  // poll limit of the hand-off waits (p.spin_cap)
+  __shared__ int s_tag;  // the launch's work-queue tag
+  __shared__ int s_seq[2][2];     // per wave group: item number of the slot's contents
+  __shared__ int s_ack[2][2];     // per wave group: waves other than 0 that have read the slot
   __shared__ int s_prefix_ready;
   // per-wave LDS rows of the whole-line K pass (kKLines)
   __shared__ __attribute__((aligned(16))) char s_kx[U::kKLines ? kMaxWaves * U::kKxBytes : 16];
 
-  const int nwaves = blockDim.x >> 6;
+  // Two items per workgroup (p.paired, instances with one query tile, two
+  // blocks in flight and the whole-line K pass): wave group grp (waves
+  // [grp W, grp W + W)) runs virtual workgroup grp * gridDim.x + blockIdx.x
+  // of the schedule below, with its own hand-off words; the LDS prefix is
+  // shared.  Both items of a CU then share one dispatch and one LDS.
+  constexpr bool kPairable = U::kKLines && NQT == 1 && NB == 2 && !TREE;
+  const bool paired = kPairable && p.paired != 0;
+  const int nw_all = blockDim.x >> 6;
+  const int nwaves = paired ? nw_all >> 1 : nw_all;  // waves per item
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int grp = paired && wave >= nwaves ? 1 : 0;
+  const int gwave = wave - grp * nwaves;  // the wave's index in its group: its first KV head
+  const int vblk = grp * (int)gridDim.x + (int)blockIdx.x;
   const int n16 = lane & 15;
   const int j = lane >> 4;
   char *const kx = s_kx + (U::kKLines ? wave * U::kKxBytes : 0);
   const int q_len = p.q_len;
   const int B = p.batch;
   const int S = p.split_size;
-  const int G = gridDim.x;
+  const int G = (paired ? 2 : 1) * (int)gridDim.x;  // virtual workgroups
   const int hpw = p.num_kv_heads / nwaves;  // units per item and wave
   const bool compact = p.compact != 0;
   // Items beyond the split-major slots of the grid go through the queue.
   // Then, in compact mode, only workgroups [0, G1) start on a split-major
-  // slot (one per CU: the first workgroup dispatched to each); workgroup
+  // slot: split 0 of sequence w, at most one per CU (the first workgroup
+  // dispatched to each), so the static round has no holes; workgroup
   // w >= G1 starts on queue item w - G1 of the compact numbering without a
   // claim.  Its page ids need the LDS prefix first, but as the second
   // workgroup on its CU its first loads would queue behind the first one's
   // K/V burst anyway, and no queue item waits for a claim in the first round.
+  // (Config 3, B = 128 on a 512-workgroup grid: G1 = 128 rather than 256
+  // leaves 384 pre-assigned items, which most of its input sets fit, so their
+  // launches claim nothing: partial kernel 45.7 -> 45.4 us.)
   const bool queued = (int64_t)G < (int64_t)B * p.num_splits;
-  const int G1 = (compact && queued) ? (G + 1) / 2 : G;
+  const int G1 = (compact && queued) ? min(B, (G + 1) / 2) : G;
   int *s_prefix = s_dyn;      // s_prefix[b]: queue items of sequences < b
   int *s_len = s_dyn + B + 1;  // clamped length of sequence b
 
@@ -998,12 +1129,12 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   int issuedU = 0;     // blocks of the current unit already loading
   bool u_loaded = false;  // page ids and query of the current unit are loading
 
-  // ---- static first item: slot blockIdx.x of the split-major numbering ----
-  int cb = (int)(blockIdx.x % (unsigned)B);
-  int cs = (int)(blockIdx.x / (unsigned)B);
+  // ---- static first item: slot vblk of the split-major numbering ----
+  int cb = (int)((unsigned)vblk % (unsigned)B);
+  int cs = (int)((unsigned)vblk / (unsigned)B);
   int cL = 0;
-  if ((int)blockIdx.x >= G1) {
-    cb = -2;  // starts on queue item blockIdx.x - G1
+  if (vblk >= G1) {
+    cb = -2;  // starts on queue item vblk - G1
   } else {
     // The query and tree words leave with the page ids and the length, before
     // any K/V load: the wait for the ids covers them, so no step waits on a
@@ -1012,7 +1143,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     // loop's static wait before the score product drained every load in flight
     // on each of its iterations.)  The ids are masked to the split once the
     // length is known.
-    load_q(cb, wave, qop);
+    load_q(cb, gwave, qop);
     load_tree(cb, treeU);
     const int start = cs * S;
     const int spec = min(S / kPage, pages_of(cb) - start / kPage);
@@ -1026,8 +1157,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // Both buffers load, a block past the unit's end reading page 0 (its
       // tiles hold page id -1), so the stream enters its loop with the loads
       // in flight of any later step.
-      load_block(buf[0], pidU, wave, 0);
-      if constexpr (NB > 1) load_block(buf[NB - 1], pidU, wave, 1);
+      load_block(buf[0], pidU, gwave, 0);
+      if constexpr (NB > 1) load_block(buf[NB - 1], pidU, gwave, 1);
       issuedU = min(nU, NB);
       u_loaded = true;
     } else {
@@ -1036,11 +1167,18 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   }
 
   if (threadIdx.x == 0) {
-    lds_put(&s_seq[0], -1);
-    lds_put(&s_seq[1], -1);
-    lds_put(&s_ack[0], nwaves - 1);  // both slots start out consumed
-    lds_put(&s_ack[1], nwaves - 1);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      lds_put(&s_seq[g][0], -1);
+      lds_put(&s_seq[g][1], -1);
+      lds_put(&s_ack[g][0], nwaves - 1);  // both slots start out consumed
+      lds_put(&s_ack[g][1], nwaves - 1);
+    }
     lds_put(&s_prefix_ready, 0);
+    lds_put(&s_cap, (int)p.spin_cap);
+    const uint64_t dp = (uint64_t)__builtin_amdgcn_dispatch_ptr();
+    lds_put(&s_tag, (int)(p.launch_tag * 0x9E3779B1u + (unsigned int)(dp >> 6) * 0x85EBCA77u +
+                          (unsigned int)(dp >> 38)));
   }
   __syncthreads();
 
@@ -1129,36 +1267,59 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // wave 0: a claim is in flight (a workgroup past the split-major round
   // holds queue item blockIdx.x - G1 as if claimed; atomic claims number
   // the items after those)
-  unsigned int claim = (int)blockIdx.x >= G1 ? blockIdx.x - (unsigned)G1 : 0u;
-  bool claimed = (int)blockIdx.x >= G1;
+  // claim: the counter's value before the atomic claim (item = its low half
+  // + G - G1), or for the pre-assigned item a negative low half vblk - G
+  // that maps to item vblk - G1 the same way (no flag: a boolean carried
+  // through the item loop cost the kernel ~60 SGPRs of spills).
+  uint64_t claim = vblk >= G1 ? (uint64_t)(uint32_t)(vblk - G) : 0u;
+  bool claimed = vblk >= G1;
   // wave 0: the queue may still hold items (never, when the static round
   // covers every slot: then no workgroup claims)
   bool more = queued;
   int t_item = 0;
   int nb = -1, ns = 0, nL = 0;
   auto issue_claim = [&]() {
-    if (lane == 0) claim = atomicAdd(&g_pd_queue[p.queue_slot][0], 1u) + (unsigned)(G - G1);
+    const unsigned int tag = (unsigned int)__builtin_amdgcn_readfirstlane(lds_poll(&s_tag));
+    if (lane == 0)
+      claim = __hip_atomic_fetch_add(&g_pd_queue[p.queue_slot][0], 1ull | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
     claimed = true;
   };
+  // Compact mode: atomic claims only when the queue holds items beyond the
+  // pre-assigned ones (a launch constant, so every workgroup decides alike:
+  // either all claim until a claim fails, or none touches the counter).  At
+  // config 3 the claims' latency depends on where the counter line sits in
+  // HBM (partial kernel 45.4-48.0 us over 64 positions), and most of its
+  // input sets need no claim at all.
+  auto claims_needed = [&]() { return !compact || queue_total() > (int64_t)(G - G1); };
   auto claim_point = [&]() {
-    if (wave == 0 && more && !claimed) issue_claim();
+    if (gwave == 0 && more && !claimed) {
+      // without the prefix yet, resolve decides after its prefix wait
+      if (compact && !__builtin_amdgcn_readfirstlane(lds_acquire(&s_prefix_ready))) return;
+      if (claims_needed()) issue_claim();
+    }
   };
   // Bounded polling: a wait loop counts its polls and stops at the limit;
   // past the loop, a wait that gave up records its error code.
-  auto spin_cap = []() { return __builtin_amdgcn_readfirstlane(uniform_ld(&g_pd_spin_limit, 0)); };
+  // The poll limit is copied into LDS at the workgroup's start and read from
+  // there when a wait starts: no register holds it across the block stream,
+  // and no wait path touches memory.  (Read from device memory, or again from
+  // the argument segment, the limit arrived only after the workgroup's K/V
+  // burst: at config 3 the waves that waited for their first item saw it ~3
+  // us late.)
+  auto spin_cap = [&]() { return (unsigned int)__builtin_amdgcn_readfirstlane(lds_poll(&s_cap)); };
   auto record_give_up = [&](unsigned int code) {
     if (lane == 0) __hip_atomic_fetch_or(&g_pd_error[p.queue_slot], code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
   // Wave 0: the next item into (db, ds, dL); db = -1 when none is left.
-  auto resolve = [&]() {
+  auto resolve_claim = [&]() {
     db = -1;
     if (!more) return;
-    if (!claimed) issue_claim();
     if (compact) {
       unsigned int polls = 0;
-      if (!__builtin_amdgcn_readfirstlane(lds_poll(&s_prefix_ready))) {
+      if (!__builtin_amdgcn_readfirstlane(lds_acquire(&s_prefix_ready))) {
         const unsigned int cap = spin_cap();
-        while (!__builtin_amdgcn_readfirstlane(lds_poll(&s_prefix_ready)) && ++polls < cap)
+        while (!__builtin_amdgcn_readfirstlane(lds_acquire(&s_prefix_ready)) && ++polls < cap)
           __builtin_amdgcn_s_sleep(1);
         if (polls < cap) polls = 0;
       }
@@ -1168,10 +1329,27 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         return;
       }
     }
+    if (!claimed) {
+      if (!claims_needed()) {
+        more = false;
+        return;
+      }
+      issue_claim();
+    }
     const int64_t Q = queue_total();
     for (;;) {
-      const int64_t c = __builtin_amdgcn_readfirstlane(claim);
+      const unsigned int lo = __builtin_amdgcn_readfirstlane((unsigned int)claim);
+      const unsigned int hi = __builtin_amdgcn_readfirstlane((unsigned int)(claim >> 32));
+      const bool atomic = (int)lo >= 0;
+      const int64_t c = (int64_t)(int)lo + (G - G1);
       claimed = false;
+      // (c < 0: a counter left flagged for ~2^31 claims without a clear; its
+      // low half now reads as a pre-assigned item)
+      if (c < 0 || (atomic && hi != lo * (unsigned int)__builtin_amdgcn_readfirstlane(lds_poll(&s_tag)))) {
+        record_give_up(L20_PD_DEVERR_QUEUE_SHARED);
+        more = false;
+        return;
+      }
       if (c >= Q) {
         more = false;
         // The launch's last atomic claim: no other atomic on the counter
@@ -1179,24 +1357,28 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         // the split-major round whose pre-assigned item fails make no atomic
         // claim, and either way the last atomic returns Q + G - 1 (after the
         // G - G1 offset; a pre-assigned failure is at most G - 1 - G1).
-        if (lane == 0 && c == Q + G - 1) g_pd_queue[p.queue_slot][0] = 0u;
+        if (atomic && lane == 0 && c == Q + G - 1) g_pd_queue[p.queue_slot][0] = 0ull;
+        // A clean launch never claims past Q + G - 1 (a second check, for a
+        // tag that happens to match).
+        if (c > Q + G - 1) record_give_up(L20_PD_DEVERR_QUEUE_SHARED);
         return;
       }
       if (decode(c)) return;
       issue_claim();  // a hole of the split-major numbering
     }
   };
+  auto resolve = [&]() { resolve_claim(); };
   // Returns true once (nb, ns, nL) holds item t_item's successor.  Wave 0
   // always completes; another wave returns false when `wait` is unset and
   // the slot is not published yet.
   auto checkpoint = [&](bool wait) {
     const int slot = t_item & 1;
-    if (wave == 0) {
+    if (gwave == 0) {
       resolve();
       unsigned int polls = 0;
-      if (__builtin_amdgcn_readfirstlane(lds_poll(&s_ack[slot])) < nwaves - 1) {
+      if (__builtin_amdgcn_readfirstlane(lds_acquire(&s_ack[grp][slot])) < nwaves - 1) {
         const unsigned int cap = spin_cap();
-        while (__builtin_amdgcn_readfirstlane(lds_poll(&s_ack[slot])) < nwaves - 1 && ++polls < cap)
+        while (__builtin_amdgcn_readfirstlane(lds_acquire(&s_ack[grp][slot])) < nwaves - 1 && ++polls < cap)
           __builtin_amdgcn_s_sleep(1);
         if (polls < cap) polls = 0;
       }
@@ -1204,23 +1386,24 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       // new one instead (valid indices, wrong results, the error recorded).
       if (__builtin_expect(polls != 0, 0)) record_give_up(L20_PD_DEVERR_ACK_WAIT);
       if (lane == 0) {
-        lds_put(&s_ack[slot], 0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the reset ahead of the publication
-        lds_put(&s_pub[slot][0], db);
-        lds_put(&s_pub[slot][1], ds);
-        lds_put(&s_pub[slot][2], dL);
-        lds_put(&s_seq[slot], t_item);  // after the item fields (LDS operations of a wave execute in order)
+        lds_put(&s_ack[grp][slot], 0);
+        lds_put(&s_pub[grp][slot][0], db);
+        lds_put(&s_pub[grp][slot][1], ds);
+        lds_put(&s_pub[grp][slot][2], dL);
+        // Release: the reset and the item fields are visible to a wave that
+        // reads this item number with acquire.
+        lds_publish(&s_seq[grp][slot], t_item);
       }
       nb = db;
       ns = ds;
       nL = dL;
       return true;
     }
-    if (__builtin_amdgcn_readfirstlane(lds_poll(&s_seq[slot])) != t_item) {
+    if (__builtin_amdgcn_readfirstlane(lds_acquire(&s_seq[grp][slot])) != t_item) {
       if (!wait) return false;
       const unsigned int cap = spin_cap();
       unsigned int polls = 0;
-      while (__builtin_amdgcn_readfirstlane(lds_poll(&s_seq[slot])) != t_item && ++polls < cap)
+      while (__builtin_amdgcn_readfirstlane(lds_acquire(&s_seq[grp][slot])) != t_item && ++polls < cap)
         __builtin_amdgcn_s_sleep(1);
       if (__builtin_expect(polls >= cap, 0)) {
         record_give_up(L20_PD_DEVERR_PUBLISH_WAIT);
@@ -1228,25 +1411,27 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         return true;
       }
     }
-    nb = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][0]));
-    ns = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][1]));
-    nL = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[slot][2]));
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // acknowledge only after the reads
-    if (lane == 0) __hip_atomic_fetch_add(&s_ack[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    nb = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[grp][slot][0]));
+    ns = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[grp][slot][1]));
+    nL = __builtin_amdgcn_readfirstlane(lds_poll(&s_pub[grp][slot][2]));
+    // Release: the reads above complete before wave 0 can see the acknowledgement.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) __hip_atomic_fetch_add(&s_ack[grp][slot], 1, L20_PD_LDS_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     return true;
   };
 
-  if (compact && more && wave == nwaves - 1) {
+  if (compact && more && wave == nw_all - 1) {
     build_prefix();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the flag follows the table (LDS operations of a wave execute in order)
-    if (lane == 0) lds_put(&s_prefix_ready, 1);
+    // Every lane stores the flag with release: each lane's own table entries
+    // are then visible to a wave whose acquire load sees the flag.
+    lds_publish(&s_prefix_ready, 1);
   }
 
   int hh = 0;
   while (cb != -1) {
     if (cb < 0) checkpoint(true);  // the static item was a hole
     if (cb >= 0) {
-      const int kvh = wave + nwaves * hh;
+      const int kvh = gwave + nwaves * hh;
       const int b = cb;
       const int L = cL;
       const int split = cs;
@@ -1300,7 +1485,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         } else if (nb >= 0) {
           hasN = true;
           nB = nb;
-          nKvh = wave;
+          nKvh = gwave;
           nN = n_blocks(ns, nL);
           pidN = load_pid(nb, ns, nL);
         }
@@ -1409,7 +1594,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         }
 
       // ---- epilogue ----
-      st.template finish<NB == 1>(p, b, kvh, direct, b, split, direct && has_ws, v_scale, n16, j);
+      st.template finish<true>(p, b, kvh, direct, b, split, direct && has_ws, v_scale, n16, j, kx);
 
       // ---- the next unit inherits the stream ----
       par = (par + nU) % NB;
@@ -1879,14 +2064,42 @@ int partial_grid(int threads, size_t lds, int64_t max_items) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, max_items));
 }
 
+// Two items per workgroup: instances with one query tile, two blocks in
+// flight and the whole-line K pass, one KV head per wave, at most 8 waves per
+// workgroup, and a launch whose persistent grid covers every split-major
+// slot (every item known from the workgroup index, none numbered through
+// the LDS prefix).  Config 2's shape (32 x 2048 tokens, 2 KV heads, 128-token
+// splits: 512 items) then runs 256 workgroups of 4 waves instead of 512 of 2:
+// 16.5-17.0 -> 15.6 us per call, fp16 partials.  With prefix-numbered items
+// (config 3) the two groups of a workgroup start their first units ~6 us
+// apart either way and pairing measured 0.5-3 us slower (timelines per
+// wave: the second item's length prefix, decode and page ids are three
+// dependent loads behind the first item's K/V burst).  L20_PD_PAIRED=0/1
+// overrides the choice (measurement).
+template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
+bool partial_paired(int num_kv_heads, int nwaves, int batch, int num_splits) {
+  constexpr bool pairable = KT != 1 && D == 128 && NQT == 1 && NB == 2 && !TREE;
+  if (!pairable || nwaves != num_kv_heads || 2 * nwaves > l20pd::kMaxWaves) return false;
+  if (const char *env = getenv("L20_PD_PAIRED")) return env[0] == '1';
+  // The paired grid (CUs workgroups of 2 x nwaves waves at occupancy 2 waves
+  // per SIMD) covers every split-major slot: no queue, no prefix.
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int64_t vslots = (int64_t)cus * (8 / nwaves);  // two virtual workgroups per workgroup
+  return (int64_t)batch * num_splits <= vslots;
+}
+
 template <typename QT, int KT, int D, int NQT, bool TREE, int NB>
 hipError_t launch_partial(l20pd::PartialParams pp, int batch, int num_kv_heads, hipStream_t stream) {
   const int nwaves = partial_waves(num_kv_heads);
-  const int threads = 64 * nwaves;
   pp.compact = partial_compact(batch) ? 1 : 0;
+  pp.paired = partial_paired<QT, KT, D, NQT, TREE, NB>(num_kv_heads, nwaves, batch, pp.num_splits) ? 1 : 0;
+  const int threads = 64 * nwaves * (pp.paired ? 2 : 1);
   const size_t lds = pp.compact ? (size_t)(2 * batch + 1) * sizeof(int) : 0;
   const int64_t max_items = (int64_t)batch * pp.num_splits;
-  const int grid = partial_grid<QT, KT, D, NQT, TREE, NB>(threads, lds, max_items);
+  // paired: each workgroup runs two virtual workgroups of the schedule
+  const int grid = partial_grid<QT, KT, D, NQT, TREE, NB>(threads, lds, pp.paired ? (max_items + 1) / 2 : max_items);
   hipLaunchKernelGGL((l20pd::pd_fp8_partial<QT, KT, D, NQT, TREE, NB>), dim3(grid), dim3(threads), lds, stream, pp);
   return hipGetLastError();
 }
@@ -2049,54 +2262,60 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   return pp;
 }
 
-// Work-queue counter slots of the split schedule, per device.  Launches on one stream run in order and share the
-// stream's slot; a launch captured into a graph takes the next slot of a
-// separate pool, since the graph may replay on any stream.  More streams in
-// use at once than eager slots share slots (least recently used first).
+// Work-queue counter slots of the split schedule, per device.  Launches on one
+// stream run in order and share the stream's slot; a launch captured into a
+// graph takes the next slot of a separate pool, since the graph may replay on
+// any stream.  More streams in use at once than eager slots share slots
+// (least recently used first; the kernel reports launches whose claims then
+// interleave).  A fixed table: taking a slot allocates nothing.  Devices past
+// kSlotDevices share the table of device % kSlotDevices (their counters are
+// still their own; only the choice of slot is shared).
 constexpr int kCaptureSlots = 16;
+constexpr int kEagerSlots = l20pd::kQueueSlots - kCaptureSlots;
+constexpr int kSlotDevices = 64;
 struct SlotEntry {
-  int dev;
-  void *stream;
-  int slot;
-  uint64_t used;
+  void *stream;   // the stream holding this slot, or null
+  uint64_t used;  // last use (g_slot_clock), 0 for a free slot
 };
 std::mutex g_slot_mu;
-std::vector<SlotEntry> g_slots;
+SlotEntry g_slots[kSlotDevices][kEagerSlots];
 uint64_t g_slot_clock = 0;
 std::atomic<unsigned int> g_capture_seq{0};
+// Launch numbers, mixed into each launch's work-queue tag.
+std::atomic<unsigned int> g_launch_seq{0};
 
 int counter_slot(hipStream_t stream) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusActive)
-    return l20pd::kQueueSlots - kCaptureSlots + (int)(g_capture_seq.fetch_add(1u) % kCaptureSlots);
+    return kEagerSlots + (int)(g_capture_seq.fetch_add(1u) % kCaptureSlots);
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  SlotEntry *tab = g_slots[dev % kSlotDevices];
   std::lock_guard<std::mutex> lock(g_slot_mu);
   const uint64_t now = ++g_slot_clock;
-  for (SlotEntry &e : g_slots)
-    if (e.dev == dev && e.stream == (void *)stream) {
-      e.used = now;
-      return e.slot;
-    }
-  constexpr int kEager = l20pd::kQueueSlots - kCaptureSlots;
-  bool taken[kEager] = {};
-  SlotEntry *lru = nullptr;
-  for (SlotEntry &e : g_slots)
-    if (e.dev == dev) {
-      taken[e.slot] = true;
-      if (!lru || e.used < lru->used) lru = &e;
-    }
-  for (int sl = 0; sl < kEager; ++sl)
-    if (!taken[sl]) {
-      g_slots.push_back(SlotEntry{dev, (void *)stream, sl, now});
+  int lru = 0;
+  for (int sl = 0; sl < kEagerSlots; ++sl) {
+    if (tab[sl].used != 0 && tab[sl].stream == (void *)stream) {
+      tab[sl].used = now;
       return sl;
     }
-  lru->stream = (void *)stream;
-  lru->used = now;
-  return lru->slot;
+    if (tab[sl].used < tab[lru].used) lru = sl;  // a free slot (used 0) wins
+  }
+  tab[lru].stream = (void *)stream;
+  tab[lru].used = now;
+  return lru;
 }
 
-
+// Poll limit of the partial kernel's hand-off waits, per device (set by
+// l20_pd_set_spin_limit, passed to every launch as a kernel argument).
+constexpr int kSpinDevices = 64;
+std::atomic<unsigned int> g_spin_limit[kSpinDevices];
+unsigned int spin_limit() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kSpinDevices) return l20pd::kSpinLimit;
+  const unsigned int v = g_spin_limit[dev].load(std::memory_order_relaxed);
+  return v ? v : l20pd::kSpinLimit;
+}
 
 l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
   l20pd::MergeParams mp;
@@ -2152,6 +2371,8 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   const int nqt = (group * a->q_len + 15) / 16;
   l20pd::PartialParams pp = partial_params(*a, n_s);
   pp.queue_slot = counter_slot(stream);
+  pp.spin_cap = spin_limit();
+  pp.launch_tag = g_launch_seq.fetch_add(1u, std::memory_order_relaxed);
   const l20pd::MergeParams mp = merge_params(*a, pp.num_splits);
   const bool bf16 = a->query_dtype == L20_PD_BF16;
   const int rows = a->batch * a->q_len;
@@ -2280,12 +2501,14 @@ int32_t l20_pd_fp8_e4m3_split_out(const l20_pd_fp8_args *a, void *stream) { retu
 
 int32_t l20_pd_set_spin_limit(uint32_t polls) {
   g_last_error[0] = '\0';
-  const unsigned int v = polls ? polls : l20pd::kSpinLimit;
-  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_spin_limit), &v, sizeof(v), 0, hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    snprintf(g_last_error, sizeof(g_last_error), "l20_pd_set_spin_limit: %s", hipGetErrorString(e));
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kSpinDevices) {
+    snprintf(g_last_error, sizeof(g_last_error), "l20_pd_set_spin_limit: %s",
+             e != hipSuccess ? hipGetErrorString(e) : "device index >= 64");
     return L20_PD_ELAUNCH;
   }
+  g_spin_limit[dev].store(polls ? polls : l20pd::kSpinLimit, std::memory_order_relaxed);
   return L20_PD_OK;
 }
 
@@ -2299,20 +2522,18 @@ int32_t l20_pd_device_errors(int32_t clear) {
     return -L20_PD_ELAUNCH;
   }
   unsigned int all = 0;
-  for (int sl = 0; sl < l20pd::kQueueSlots; ++sl) {
-    all |= err[sl];
-    if (clear && err[sl]) {
-      // a launch that gave up may have left its work-queue counter mid-way
-      const unsigned int zero[16] = {0};
-      const unsigned int none = 0;
-      e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_queue), zero, sizeof(zero), sizeof(zero) * sl, hipMemcpyHostToDevice);
-      if (e == hipSuccess)
-        e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_error), &none, sizeof(none), sizeof(none) * sl,
-                              hipMemcpyHostToDevice);
-      if (e != hipSuccess) {
-        snprintf(g_last_error, sizeof(g_last_error), "l20_pd_device_errors: %s", hipGetErrorString(e));
-        return -L20_PD_ELAUNCH;
-      }
+  for (int sl = 0; sl < l20pd::kQueueSlots; ++sl) all |= err[sl];
+  if (clear) {
+    // A launch that gave up (or two that shared a slot) may have left a
+    // work-queue counter mid-way: every slot's counter and error word start
+    // from zero again.
+    static const unsigned int zero[sizeof(l20pd::g_pd_queue) / sizeof(unsigned int)] = {0};
+    e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_queue), zero, sizeof(l20pd::g_pd_queue), 0, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_error), zero, sizeof(l20pd::g_pd_error), 0, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      snprintf(g_last_error, sizeof(g_last_error), "l20_pd_device_errors: %s", hipGetErrorString(e));
+      return -L20_PD_ELAUNCH;
     }
   }
   return (int32_t)all;

@@ -18,6 +18,7 @@ L20_PD_BF16, L20_PD_FP16, L20_PD_FP32 = 0, 1, 2
 L20_PD_OK, L20_PD_EINVAL, L20_PD_ELAUNCH = 0, 1, 2
 L20_PD_KV_FP8_E4M3, L20_PD_KV_FP16, L20_PD_KV_BF16, L20_PD_KV_FP8_E5M2 = 0, 1, 2, 3
 L20_PD_DEVERR_PREFIX_WAIT, L20_PD_DEVERR_ACK_WAIT, L20_PD_DEVERR_PUBLISH_WAIT = 1, 2, 4
+L20_PD_DEVERR_QUEUE_SHARED = 32
 ABI_VERSION = 4
 
 # Every extern "C" symbol declared in include/*.h.

@@ -3,11 +3,17 @@
 * Bounded hand-off waits: with a spin limit of one poll (set from the host
   with l20_pd_set_spin_limit) the waits between the waves of a workgroup give
   up at once; every kernel still exits normally, the give-up is reported through
-  l20_pd_device_errors, and after clearing it the next call is exact again.
+  l20_pd_device_errors (with the queue-sharing error when a give-up left the
+  work-queue counter mid-way), and after clearing, which also zeroes the
+  counters, the next call is exact again.
 * Counter slots: graph replays of a queue-driven call interleaved with eager
   queue-driven calls on another stream, each bitwise equal to its eager
   result (a graph's captured launch and the other stream's launches hold
   different work-queue slots).
+* Counter sharing: two graphs captured 16 captures apart (one capture slot)
+  replayed at the same time on two streams: every replay's results are
+  bitwise exact, or the sharing is reported (L20_PD_DEVERR_QUEUE_SHARED), and
+  after clearing, an eager call is exact again.
 * Graph soak: one captured config-3 call replayed 1000 times, every replay
   bitwise equal to the eager call (the reference's stress of this op:
   scripts/stress_cuda_paged_decode.py:160-166, 1000 replays).
@@ -51,7 +57,11 @@ def test_hand_off_waits_give_up_and_report(monkeypatch):
     finally:
         cabi.set_spin_limit(0)
     err = cabi.device_errors(clear=False)
-    assert err != 0 and err & ~7 == 0, err
+    # Wait give-ups (1, 2, 4).  A workgroup that gave up at the prefix wait
+    # abandons a claim it had issued, so that launch never reaches its last
+    # claim and leaves the counter mid-way: the next call reports
+    # L20_PD_DEVERR_QUEUE_SHARED, and clearing zeroes the counter.
+    assert err & 7 != 0 and err & ~(7 | cabi.L20_PD_DEVERR_QUEUE_SHARED) == 0, err
     assert cabi.device_errors(clear=True) == err
     assert cabi.device_errors() == 0
     # recovered: the same call with the normal limit is exact again
@@ -111,6 +121,85 @@ def test_graph_replays_interleaved_with_eager_launches_on_another_stream(monkeyp
     assert not bad_a and not bad_b, (bad_a, bad_b)
     assert torch.equal(lse_a, ref_a[1]) and torch.equal(lse_b, ref_b[1])
     assert cabi.device_errors() == 0
+
+
+def test_graphs_sharing_a_counter_slot_are_exact_or_reported(monkeypatch):
+    import l20_pd_cabi as cabi
+
+    assert cabi.device_errors(clear=True) == 0, "a device error was pending before this test"
+    # A long queue-driven call: 4 workgroups drain ~500 items each replay, so
+    # two replays started together overlap for most of their claims.
+    monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", "4")
+    big = H.make_synthetic(8, 16, 2, 128, [4000, 3900, 4096, 3500, 4001, 3777, 4090, 3999], seed=31)
+    tiny = H.make_synthetic(1, 16, 2, 128, [40], seed=32)
+    split = 64
+    outs = [torch.empty_like(big["query"]) for _ in range(2)]
+    lses = [torch.empty(big["query"].shape[:2], dtype=torch.float32, device="cuda") for _ in range(2)]
+    # every replay starts from zeroed outputs and partials, so an item that a
+    # replay skipped cannot be covered by an earlier replay's partials
+    wss = [H.workspace(big, split) for _ in range(2)]
+    args_big = [cabi.args_from_tensors(big["query"], big["key_cache"], big["value_cache"], big["block_table"],
+                                       big["seq_lens"], *wss[i], outs[i], big["k_scale"], big["v_scale"],
+                                       big["max_seq_len"], split, softmax_scale=big["softmax_scale"], lse=lses[i])
+                for i in range(2)]
+
+    def zero(i):
+        for t in (outs[i], lses[i]) + tuple(wss[i]):
+            t.zero_()
+
+    out_t = torch.empty_like(tiny["query"])
+    lse_t = torch.empty(tiny["query"].shape[:2], dtype=torch.float32, device="cuda")
+    args_tiny = _call_args(tiny, split, out_t, lse_t)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        cabi.split_out(args_big[0], stream.cuda_stream)
+    torch.cuda.synchronize()
+    ref = (outs[0].clone(), lses[0].clone())
+    H.compare(*ref, *H.run_oracle(big))
+    # 17 consecutive captures take the 16 capture slots in turn: the first and
+    # the last share one.
+    graphs = []
+    for k in range(17):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                if k == 0:
+                    cabi.split_out(args_big[0], stream.cuda_stream)
+                elif k == 16:
+                    cabi.split_out(args_big[1], stream.cuda_stream)
+                else:
+                    cabi.split_out(args_tiny, stream.cuda_stream)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    reported = exact = 0
+    for rep in range(6):
+        zero(0)
+        zero(1)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(sa):
+            graphs[0].replay()
+        with torch.cuda.stream(sb):
+            graphs[16].replay()
+        torch.cuda.synchronize()
+        err = cabi.device_errors(clear=True)  # also zeroes the counters
+        ok = all(torch.equal(outs[i], ref[0]) and torch.equal(lses[i], ref[1]) for i in range(2))
+        assert err & ~cabi.L20_PD_DEVERR_QUEUE_SHARED == 0, err
+        assert ok or err == cabi.L20_PD_DEVERR_QUEUE_SHARED, f"replay {rep}: wrong results and no report"
+        reported += err != 0
+        exact += ok
+    print(f"overlapping replays on one slot: {reported} of 6 reported, {exact} of 6 exact", flush=True)
+    # after the clear, the slot serves calls again
+    for i, g in ((0, graphs[0]), (1, graphs[16])):
+        zero(i)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(sa):
+            g.replay()
+        torch.cuda.synchronize()
+        assert cabi.device_errors() == 0
+        assert torch.equal(outs[i], ref[0]) and torch.equal(lses[i], ref[1]), i
 
 
 def test_graph_replay_soak_at_headline_scale():
