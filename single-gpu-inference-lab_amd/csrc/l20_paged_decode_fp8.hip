@@ -1650,6 +1650,36 @@ __device__ __forceinline__ void load_partial8(const void *po, int64_t off, f32x4
   }
 }
 
+// The same eight elements as raw bits (two 16-byte words for fp32, one for
+// 16-bit elements), converted by unpack_partial8 where they are used: a
+// conversion next to the load would make the wave wait for it there.
+template <int PK>
+__device__ __forceinline__ void load_partial8_raw(const void *po, int64_t off, i32x4 &r0, i32x4 &r1) {
+  if constexpr (PK == 0) {
+    const i32x4 *src = reinterpret_cast<const i32x4 *>(reinterpret_cast<const float *>(po) + off);
+    r0 = src[0];
+    r1 = src[1];
+  } else {
+    r0 = *reinterpret_cast<const i32x4 *>(reinterpret_cast<const uint16_t *>(po) + off);
+    r1 = i32x4{0, 0, 0, 0};
+  }
+}
+template <int PK>
+__device__ __forceinline__ void unpack_partial8(i32x4 r0, i32x4 r1, f32x4 &a, f32x4 &b) {
+  if constexpr (PK == 0) {
+    a = __builtin_bit_cast(f32x4, r0);
+    b = __builtin_bit_cast(f32x4, r1);
+  } else if constexpr (PK == 1) {
+    const f16x8 v = __builtin_bit_cast(f16x8, r0);
+    a = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    b = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+  } else {
+    const bf16x8 v = __builtin_bit_cast(bf16x8, r0);
+    a = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    b = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+  }
+}
+
 struct MergeParams {
   const void *po;
   int64_t po_srow, po_shead, po_ssplit;
@@ -1682,7 +1712,10 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   __shared__ float s_m[WPB], s_w[WPB];
   __shared__ f32x4 s_acc[WPP > 1 ? WPB : 1][CH][2];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform (SGPR): the row, its length and the step tests below are
+  // scalar, so a test around a step's loads is a scalar branch, not an
+  // exec-masked one that waits for every load before the next step's
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wp = wave % WPP;
   const int c = lane % CH;
   const int g = lane / CH;
@@ -1691,14 +1724,28 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   const bool live = pair < (uint32_t)(p.rows * p.num_q_heads);
   const int row = live ? (int)(pair / (uint32_t)p.num_q_heads) : 0;
   const int h = live ? (int)(pair - (uint32_t)row * (uint32_t)p.num_q_heads) : 0;
+  const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
+  const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
+  const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
+  // The first step's slot of each lane group loads before the row's split
+  // count is known, in the round trip of the sequence length (slot 0 past
+  // the workspace; a slot past the count is not folded): rows of at most
+  // SG * WPP splits then take one round trip less.
+  float m_pre, l_pre;
+  i32x4 r0_pre, r1_pre;
+  {
+    const int s = wp * SG + g;
+    const int sl = s < p.num_splits ? s : 0;
+    m_pre = pm[(int64_t)sl * p.pm_ssplit];
+    l_pre = pl[(int64_t)sl * p.pl_ssplit];
+    load_partial8_raw<PK>(p.po, base + (int64_t)sl * p.po_ssplit, r0_pre, r1_pre);
+  }
   int n = 0;
   if (live) {
     const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
     n = (L > 0) ? (L + p.split_size - 1) / p.split_size : 0;
   }
   if (WPP == 1 && n <= 1) return;  // the partial kernel wrote this row (or the empty row) directly
-  const float *pm = p.pm + (int64_t)row * p.pm_srow + (int64_t)h * p.pm_shead;
-  const float *pl = p.pl + (int64_t)row * p.pl_srow + (int64_t)h * p.pl_shead;
   // Online merge (max, weight sum, weighted rows) over the lane's slots; NaN
   // slots (a run continued from an earlier slot) never enter the sums.
   // final_row: one run wrote the whole row already (slot 0's m is +inf).  Only
@@ -1708,39 +1755,58 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   bool final_row = false;
   float mx = -INFINITY, wsum = 0.0f;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  const int64_t base = (int64_t)row * p.po_srow + (int64_t)h * p.po_shead + 8 * c;
   const int n_here = n > 1 ? n : 0;
   // Steps of a wave in groups of kSteps: every load of a group is issued
-  // before the group is folded (one round trip for up to kSteps steps); a
-  // slot past the row's count loads slot 0, which exists whenever n > 1, and
-  // is not folded.  (Against a loop unrolled by two with the loads under the
-  // slot test: call minus partial kernel 5.76 -> 5.57 us at config 3, 8.2 ->
+  // before the group is folded (one round trip for up to kSteps steps); in a
+  // step that reaches the row's count, a slot past it loads slot 0, which
+  // exists whenever n > 1, and is not folded; a step wholly past it loads
+  // nothing.  (Against a loop unrolled by two with the loads under the slot
+  // test: call minus partial kernel 5.76 -> 5.57 us at config 3, 8.2 ->
   // 7.65 us at config 4.)
   constexpr int kSteps = 4;
-  for (int s0 = wp * SG; s0 < n_here; s0 += kSteps * WPP * SG) {
-    float ms[kSteps], ls[kSteps];
-    f32x4 o0[kSteps], o1[kSteps];
-#pragma unroll
-    for (int k = 0; k < kSteps; ++k) {
-      const int s = s0 + k * WPP * SG + g;
-      const int sl = s < n_here ? s : 0;
-      ms[k] = pm[(int64_t)sl * p.pm_ssplit];
-      ls[k] = pl[(int64_t)sl * p.pl_ssplit];
-      const int64_t off = base + (int64_t)sl * p.po_ssplit;
-      load_partial8<PK>(p.po, off, o0[k], o1[k]);
+  auto fold = [&](int s, float m, float l, f32x4 a0, f32x4 a1) {
+    if (s < n_here && m == m && m != -INFINITY) {
+      const float m_new = fmaxf(mx, m);
+      const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
+      const float w = __builtin_amdgcn_exp2f(m - m_new) * l;
+      acc0 = acc0 * a_old + w * a0;
+      acc1 = acc1 * a_old + w * a1;
+      wsum = wsum * a_old + w;
+      mx = m_new;
     }
-    if (s0 == 0 && ms[0] == INFINITY) final_row = true;
+  };
+  for (int s0 = wp * SG; s0 < n_here; s0 += kSteps * WPP * SG) {
+    // the first group's step 0 is the preload, folded from its own
+    // registers (a copy would wait for it before the later steps' loads)
+    const bool first = s0 == wp * SG;
+    float ms[kSteps], ls[kSteps];
+    i32x4 r0[kSteps], r1[kSteps];
+    // the group's remaining steps load together, or (a row that the
+    // preloaded step covers: a wave-uniform test) not at all
+    const bool rest = !first || n_here > s0 + WPP * SG;
+    if (rest) {
+#pragma unroll
+      for (int k = 0; k < kSteps; ++k) {
+        if (k == 0 && first) continue;
+        const int s = s0 + k * WPP * SG + g;
+        const int sl = s < n_here ? s : 0;
+        ms[k] = pm[(int64_t)sl * p.pm_ssplit];
+        ls[k] = pl[(int64_t)sl * p.pl_ssplit];
+        load_partial8_raw<PK>(p.po, base + (int64_t)sl * p.po_ssplit, r0[k], r1[k]);
+      }
+    }
+    if (first) {
+      if (s0 == 0 && m_pre == INFINITY) final_row = true;
+      f32x4 a0, a1;
+      unpack_partial8<PK>(r0_pre, r1_pre, a0, a1);
+      fold(s0 + g, m_pre, l_pre, a0, a1);
+    }
 #pragma unroll
     for (int k = 0; k < kSteps; ++k) {
-      if (s0 + k * WPP * SG + g < n_here && ms[k] == ms[k] && ms[k] != -INFINITY) {
-        const float m_new = fmaxf(mx, ms[k]);
-        const float a_old = __builtin_amdgcn_exp2f(mx - m_new);  // 0 while mx == -inf
-        const float w = __builtin_amdgcn_exp2f(ms[k] - m_new) * ls[k];
-        acc0 = acc0 * a_old + w * o0[k];
-        acc1 = acc1 * a_old + w * o1[k];
-        wsum = wsum * a_old + w;
-        mx = m_new;
-      }
+      if ((k == 0 && first) || !rest) continue;
+      f32x4 a0, a1;
+      unpack_partial8<PK>(r0[k], r1[k], a0, a1);
+      fold(s0 + k * WPP * SG + g, ms[k], ls[k], a0, a1);
     }
   }
   // LSE-combine (mx, wsum, acc) with another partial state.
