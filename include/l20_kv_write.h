@@ -35,7 +35,10 @@ extern "C" {
  *   cos_sin_cache  [max_position, rotary_dim] cs_dtype: cos in the first half, sin in the second
  *   slot_mapping   [num_tokens] int64: cache page slot // 16, row slot % 16; < 0 skips the token
  *   key/value_cache[num_pages, 16, num_kv_heads, head_dim] cache_dtype (enum l20_pd_kv_dtype;
- *                  a 16-bit cache must have the model dtype)
+ *                  a 16-bit cache must have the model dtype).  A cache of P-token pages
+ *                  (P a multiple of 16, tokens contiguous) is passed as its 16-token
+ *                  sub-pages: num_pages * P / 16 pages, stride_page = 16 * stride_token;
+ *                  slot s (page s // P, row s % P) is then sub-page s // 16, row s % 16
  *
  * x' = x cos + (x_pair sin) sign on the first rotary_dim dims (each product
  * and the sum rounded to fp32, the result rounded to dtype), pairs

@@ -70,8 +70,11 @@ enum l20_pd_status {
  * every tensor (head_dim) must be contiguous.
  *
  *   query          [batch*q_len, num_q_heads, head_dim]   bf16 or fp16
- *   key/value      [num_pages, page_size=16, num_kv_heads, head_dim]  e4m3fn bytes
- *   block_table    [batch, >= ceil(max_seq_len/16)]  int32 physical page ids, or,
+ *   key/value      [num_pages, page_size, num_kv_heads, head_dim]  e4m3fn bytes; page_size
+ *                  any multiple of 16 through 4096 (above 16 a page's tokens must be
+ *                  contiguous: stride_page = page_size * stride_token); token t of a
+ *                  sequence is row t % page_size of page block_table[b][t / page_size]
+ *   block_table    [batch, >= ceil(max_seq_len/page_size)]  int32 physical page ids, or,
  *                  with page_indptr [batch+1] (CSR), the flat page list: sequence b's
  *                  pages are block_table[page_indptr[b] .. page_indptr[b+1])
  *   seq_lens       [batch]  int32, each <= max_seq_len, includes the q_len new tokens

@@ -119,7 +119,7 @@ def rope_and_cache(
 
     query/key/value [T, H, D] float32 holding model-dtype values; positions and
     slot_mapping [T] ints; cos_sin_cache [P, rotary_dim] float32 (model-dtype
-    values); caches [pages, 16, Hkv, D]: uint8 codes when ``cache_fp8`` else
+    values); caches [pages, P, Hkv, D] (P-token pages): uint8 codes when ``cache_fp8`` else
     float32 holding model-dtype values."""
     rotary_dim = cos_sin_cache.shape[1]
     cs = np.asarray(cos_sin_cache, dtype=np.float32)[np.asarray(positions)]
@@ -130,9 +130,10 @@ def rope_and_cache(
     vc = np.array(value_cache, copy=True)
     k_store = quantize_rows(k_out, k_scale) if cache_fp8 else k_out
     v_store = quantize_rows(v_in, v_scale) if cache_fp8 else v_in
+    page = kc.shape[1]  # tokens per page
     for t, slot in enumerate(np.asarray(slot_mapping)):
         if slot < 0:
             continue
-        kc[slot // pd.PAGE_SIZE, slot % pd.PAGE_SIZE] = k_store[t]
-        vc[slot // pd.PAGE_SIZE, slot % pd.PAGE_SIZE] = v_store[t]
+        kc[slot // page, slot % page] = k_store[t]
+        vc[slot // page, slot % page] = v_store[t]
     return q_out, k_out, kc, vc

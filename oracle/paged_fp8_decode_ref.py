@@ -11,7 +11,7 @@ What it restates (reference file:line, relative to the reference repo root):
   per-tensor ``scale = max(amax / 448, 1e-12)``, ``clamp(+-448)``, round to
   e4m3fn.  The per-head variant applies the same rule to each KV head.
 * ``reference``         -- ``scripts/smoke_cuda_paged_fp8_decode_op.py:22-41``:
-  gather ``block_table[b, t // 16]`` / ``t % 16``, dequantise in fp32
+  gather ``block_table[b, t // P]`` / ``t % P`` (P-token pages, 16 by default), dequantise in fp32
   (``code * scale``), repeat each KV head over its GQA group, softmax of
   ``q . k * softmax_scale`` and the probability-weighted sum of V.  Extended
   (closed-form, see below) to per-head scales, any softmax scale, head_dim 64,
@@ -204,10 +204,13 @@ def _head_scales(scale: ScaleLike, num_kv_heads: int) -> np.ndarray:
 
 
 def gather_pages(cache: np.ndarray, table_row: np.ndarray, length: int) -> np.ndarray:
-    """Logical tokens ``0..length-1`` of one sequence: ``cache[table[t//16], t%16]``."""
+    """Logical tokens ``0..length-1`` of one sequence: ``cache[table[t // P], t % P]``
+    for a cache of ``P``-token pages ``[pages, P, Hkv, D]`` (``P = cache.shape[1]``; the
+    reference hook's page geometry, ``integrations/vllm/l20_paged_split_kv.py:156,182-200``)."""
+    page = cache.shape[1]
     token = np.arange(length)
-    physical = np.asarray(table_row)[token // PAGE_SIZE]
-    return cache[physical, token % PAGE_SIZE]
+    physical = np.asarray(table_row)[token // page]
+    return cache[physical, token % page]
 
 
 def dequantize(codes: np.ndarray, scale: ScaleLike, head_axis: int = -2, kv_format: str = "e4m3fn") -> np.ndarray:
@@ -310,7 +313,7 @@ def reference(
     """Dequantise-then-attend (``smoke_cuda_paged_fp8_decode_op.py:22-41``).
 
     query       [B*q_len, Hq, D] float (bf16/fp16 values held as float32)
-    key/value   [P, 16, Hkv, D] uint8 codes of ``kv_format`` (e4m3fn or e5m2)
+    key/value   [pages, P, Hkv, D] uint8 codes of ``kv_format`` (e4m3fn or e5m2), P-token pages
     block_table [B, max_pages] int (or the flat page list with ``page_indptr`` [B+1])
     seq_lens    [B] int;  k/v_scale float or [Hkv]
     Row ``b*q_len + i`` attends to keys ``0 .. L_b - q_len + i``.
@@ -469,6 +472,7 @@ def brute_force_fp64(
     decode = [float(v) for v in (e4m3fn_decode_table() if kv_format == "e4m3fn" else e5m2_decode_table())]
     out = np.zeros((n_rows, num_q_heads, head_dim))
     lse = np.full((n_rows, num_q_heads), -np.inf)
+    page_tokens = key_cache.shape[1]
     for r in range(n_rows):
         b, i = divmod(r, q_len)
         length = int(seq_lens[b])
@@ -482,8 +486,8 @@ def brute_force_fp64(
             kvh = h // group
             scores = []
             for t in keys:
-                page = int(block_table[b][t // PAGE_SIZE])
-                slot = t % PAGE_SIZE
+                page = int(block_table[b][t // page_tokens])
+                slot = t % page_tokens
                 dot = 0.0
                 for d in range(head_dim):
                     k = decode[int(key_cache[page, slot, kvh, d])] * float(ks[kvh])
@@ -496,8 +500,8 @@ def brute_force_fp64(
             total = sum(weights)
             lse[r, h] = top + math.log(total)
             for t, w in zip(keys, weights):
-                page = int(block_table[b][t // PAGE_SIZE])
-                slot = t % PAGE_SIZE
+                page = int(block_table[b][t // page_tokens])
+                slot = t % page_tokens
                 for d in range(head_dim):
                     v = decode[int(value_cache[page, slot, kvh, d])] * float(vs[kvh])
                     out[r, h, d] += w / total * v

@@ -79,9 +79,10 @@ def reference_torch(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
         if length <= 0:
             continue
         t = torch.arange(length)
-        pages = block_table[b].long()[t // PAGE_SIZE]
-        keys = _scaled(key_cache[pages, t % PAGE_SIZE], k_scale)      # [L, Hkv, D]
-        values = _scaled(value_cache[pages, t % PAGE_SIZE], v_scale)  # [L, Hkv, D]
+        page = key_cache.shape[1]  # tokens per page
+        pages = block_table[b].long()[t // page]
+        keys = _scaled(key_cache[pages, t % page], k_scale)      # [L, Hkv, D]
+        values = _scaled(value_cache[pages, t % page], v_scale)  # [L, Hkv, D]
         # [Hkv, q_len * G, D]: query row i, head kvh * G + g
         q = q_all[b * q_len:(b + 1) * q_len].view(q_len, hkv, group, d).permute(1, 0, 2, 3).reshape(
             hkv, q_len * group, d)

@@ -109,7 +109,7 @@ struct PartialParams {
   float qk_scale_log2;  // softmax_scale * log2(e)
   int q_len, num_q_heads, num_kv_heads, group, split_size, num_splits;
   int po_kind;  // partial o/l element: 0 fp32, 1 fp16, 2 bf16
-  int l_cap;  // min(num_splits * split_size, block-table pages * 16): tokens past it are never touched
+  int l_cap;  // min(num_splits * split_size, block-table pages * page_size): tokens past it are never touched
   int batch;
   int bt_pages;  // block-table row length
   int compact;   // queue items numbered through an LDS prefix
@@ -126,6 +126,15 @@ struct PartialParams {
   unsigned int spin_cap;
   // Host launch number, mixed into the launch's work-queue tag.
   unsigned int launch_tag;
+  // 16-token tiles per page-list entry (pages of 16 * page_mult tokens, their
+  // tokens contiguous): tile T of a sequence is sub-page T % page_mult of
+  // entry T / page_mult, virtual page entry * page_mult + T % page_mult of a
+  // cache seen as 16-token pages (num_pages and the page stride are given in
+  // those).
+  int page_mult;
+  // ceil(2^32 / page_mult) (page_mult > 1): T / page_mult = umulhi(T, magic),
+  // exact for T < 2^32 / page_mult (the host bounds max_seq_len for it).
+  unsigned int page_magic;
 };
 
 // ---------------------------------------------------------------------------
@@ -1094,17 +1103,29 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   auto pages_of = [&](int b) {
     return p.indptr ? uniform_ld(p.indptr, b + 1) - uniform_ld(p.indptr, b) : p.bt_pages;
   };
+  // Virtual 16-token page of tile T of a page list; -1 for an entry outside
+  // the cache (checked in 64 bits, before any product can wrap).
+  auto tile_page = [&](const int32_t *row, int T) -> int {
+    const int m = p.page_mult;
+    if (__builtin_expect(m == 1, 1)) {
+      const int e = row[T];
+      return (e >= 0 && (int64_t)e < p.num_pages) ? e : -1;
+    }
+    const int q = (int)__umulhi((unsigned int)T, p.page_magic);  // T / m
+    const int e = row[q];
+    const int64_t v = (int64_t)e * m + (T - q * m);
+    return (e >= 0 && v < p.num_pages) ? (int)v : -1;
+  };
   // Page ids of split s of sequence b: lane t -> tile t (a split has <= 64
   // tiles); -1 for tiles past the split, past the page list, and for
   // out-of-range ids.
   auto load_pid = [&](int b, int s, int L) {
     const int start = s * S;
     const int tiles = max(0, (min(start + S, L) - start + kPage - 1) / kPage);
-    const int avail = pages_of(b) - start / kPage;
+    const int avail = pages_of(b) * p.page_mult - start / kPage;
     int v = -1;
     if (lane < tiles && lane < avail) {
-      v = row_of(b)[start / kPage + lane];
-      v = (v >= 0 && (int64_t)v < p.num_pages) ? v : -1;
+      v = tile_page(row_of(b), start / kPage + lane);
     }
     return v;
   };
@@ -1146,9 +1167,9 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
     load_q(cb, gwave, qop);
     load_tree(cb, treeU);
     const int start = cs * S;
-    const int spec = min(S / kPage, pages_of(cb) - start / kPage);
+    const int spec = min(S / kPage, pages_of(cb) * p.page_mult - start / kPage);
     int v = -1;
-    if (lane < spec) v = row_of(cb)[start / kPage + lane];
+    if (lane < spec) v = tile_page(row_of(cb), start / kPage + lane);
     cL = clamped_len(p, cb);
     if (cs < splits_of_len(cL, S)) {
       const int tiles = max(0, (min(start + S, cL) - start + kPage - 1) / kPage);
@@ -2028,7 +2049,10 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   const int64_t es = kv16 ? 2 : 1;  // bytes per cache element
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(L20_PD_EINVAL, "NHD cache only: head_dim must be 64 or 128");
-  if (a->page_size != 16) return fail(L20_PD_EINVAL, "NHD cache only: page_size must be 16");
+  // Pages of any multiple of 16 tokens (the reference's vLLM hook passes its
+  // block size through, integrations/vllm/l20_paged_split_kv.py:156,182-200).
+  if (a->page_size < 16 || a->page_size % 16 != 0 || a->page_size > 4096)
+    return fail(L20_PD_EINVAL, "NHD cache only: page_size must be a multiple of 16 from 16 through 4096");
   if (a->num_kv_heads <= 0 || a->num_q_heads <= 0)
     return fail(L20_PD_EINVAL, "head counts must be positive");
   if (a->num_q_heads % a->num_kv_heads != 0)
@@ -2050,6 +2074,16 @@ int32_t check_args(const l20_pd_fp8_args *a) {
   if (((uintptr_t)a->tree_mask % 4) != 0 || a->tree_mask_stride_batch < 0)
     return fail(L20_PD_EINVAL, "tree_mask must be int32 [batch, q_len] (batch stride >= 0)");
   if (a->num_pages <= 0) return fail(L20_PD_EINVAL, "K/V cache has no pages");
+  if (a->page_size > 16) {
+    // read as 16-token sub-pages: a page's tokens must be contiguous
+    if (a->k_stride_page != a->page_size * a->k_stride_token || a->v_stride_page != a->page_size * a->v_stride_token)
+      return fail(L20_PD_EINVAL, "pages of more than 16 tokens must hold them contiguously (stride_page = page_size x stride_token)");
+    if (a->num_pages * (a->page_size / 16) > INT32_MAX || (int64_t)a->bt_max_pages * a->page_size > INT32_MAX)
+      return fail(L20_PD_EINVAL, "K/V cache and block table must hold fewer than 2^35 tokens");
+    // the kernels divide 16-token tile indices by page_size / 16 through a reciprocal
+    if ((int64_t)a->max_seq_len / 16 + 128 >= (((int64_t)1 << 32) / (a->page_size / 16)))
+      return fail(L20_PD_EINVAL, "max_seq_len is too long for this page_size");
+  }
   const int32_t n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
   if (n_s > 1) {
     if (!a->partial_output || !a->partial_max || !a->partial_sum)
@@ -2064,7 +2098,7 @@ int32_t check_args(const l20_pd_fp8_args *a) {
     if (st < 0 || sh < 0 || (15 * st + (int64_t)(a->num_kv_heads - 1) * sh + a->head_dim) * es > INT32_MAX)
       return fail(L20_PD_EINVAL, "K/V token and head strides must be non-negative and span less than 2 GiB per page");
   }
-  if (!a->page_indptr && a->bt_max_pages * (int64_t)16 < a->max_seq_len)
+  if (!a->page_indptr && a->bt_max_pages * (int64_t)a->page_size < a->max_seq_len)
     return fail(L20_PD_EINVAL, "block table has fewer pages than max_seq_len needs");
   // Vector-load alignment: 16 B K chunks, V chunks of head_dim/16 elements, 16 B query chunks.
   const uint64_t kbits = (uint64_t)(uintptr_t)a->key_cache | (uint64_t)(a->k_stride_page * es) |
@@ -2261,7 +2295,7 @@ hipError_t launch_merge(const l20pd::MergeParams &mp, int rows, int heads, hipSt
 int length_cap(const l20_pd_fp8_args &a, int num_splits) {
   const int64_t by_splits = (int64_t)num_splits * a.split_size;
   if (a.page_indptr) return (int)by_splits;
-  return (int)std::min<int64_t>(by_splits, (int64_t)a.bt_max_pages * 16);
+  return (int)std::min<int64_t>(by_splits, (int64_t)a.bt_max_pages * a.page_size);
 }
 
 l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
@@ -2272,12 +2306,17 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.q_shead = a.q_stride_head;
   // The kernels address the caches in bytes.
   const int64_t es = (a.kv_dtype == L20_PD_KV_FP16 || a.kv_dtype == L20_PD_KV_BF16) ? 2 : 1;
+  // Pages of 16 m tokens are read as m 16-token sub-pages (contiguous, as
+  // check_args requires): m times the pages, each 16 token strides apart.
+  const int m = a.page_size / 16;
+  pp.page_mult = m;
+  pp.page_magic = m > 1 ? (unsigned int)((((uint64_t)1 << 32) + m - 1) / m) : 0u;
   pp.k = a.key_cache;
-  pp.k_spage = a.k_stride_page * es;
+  pp.k_spage = (m == 1 ? a.k_stride_page : 16 * a.k_stride_token) * es;
   pp.k_stok32 = (int)(a.k_stride_token * es);
   pp.k_shead32 = (int)(a.k_stride_head * es);
   pp.v = a.value_cache;
-  pp.v_spage = a.v_stride_page * es;
+  pp.v_spage = (m == 1 ? a.v_stride_page : 16 * a.v_stride_token) * es;
   pp.v_stok32 = (int)(a.v_stride_token * es);
   pp.v_shead32 = (int)(a.v_stride_head * es);
   // Bytes one KV-head slice of a page can touch: the buffer range of its loads.
@@ -2286,7 +2325,7 @@ l20pd::PartialParams partial_params(const l20_pd_fp8_args &a, int n_s) {
   pp.bt = a.block_table;
   pp.bt_srow = a.bt_stride_row;
   pp.seq_lens = a.seq_lens;
-  pp.num_pages = a.num_pages;
+  pp.num_pages = a.num_pages * m;
   pp.po = a.partial_output;
   pp.po_srow = a.po_stride_row;
   pp.po_shead = a.po_stride_head;

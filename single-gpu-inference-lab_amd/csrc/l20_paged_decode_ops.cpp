@@ -309,7 +309,14 @@ l20_pd_kv_write_args kv_args(const std::optional<at::Tensor> &query, const at::T
   }
   TORCH_CHECK(key_cache.dim() == 4 && value_cache.sizes() == key_cache.sizes(),
               "cache must use NHD [blocks, block, heads, dim]");
-  TORCH_CHECK(key_cache.size(1) == 16, "cache must use NHD [blocks, block, heads, dim]");
+  // Pages of any multiple of 16 tokens; a page of 16 m tokens is written as m
+  // 16-token sub-pages (slot s is sub-page s / 16, row s % 16), which needs
+  // its tokens contiguous.
+  const int64_t page_tokens = key_cache.size(1);
+  TORCH_CHECK(page_tokens >= 16 && page_tokens % 16 == 0, "cache block size must be a multiple of 16");
+  TORCH_CHECK(page_tokens == 16 || (key_cache.stride(0) == page_tokens * key_cache.stride(1) &&
+                                    value_cache.stride(0) == page_tokens * value_cache.stride(1)),
+              "cache blocks of more than 16 tokens must hold them contiguously");
   TORCH_CHECK(key_cache.size(2) == key.size(1) && key_cache.size(3) == key.size(2),
               "cache head shape must match K/V");
   const bool fp8 = key_cache.scalar_type() == at::kFloat8_e4m3fn;
@@ -350,14 +357,14 @@ l20_pd_kv_write_args kv_args(const std::optional<at::Tensor> &query, const at::T
   a.is_neox = is_neox ? 1 : 0;
   a.slot_mapping = slot_mapping.data_ptr<int64_t>();
   a.key_cache = key_cache.data_ptr();
-  a.kc_stride_page = key_cache.stride(0);
+  a.kc_stride_page = page_tokens == 16 ? key_cache.stride(0) : 16 * key_cache.stride(1);
   a.kc_stride_token = key_cache.stride(1);
   a.kc_stride_head = key_cache.stride(2);
   a.value_cache = value_cache.data_ptr();
-  a.vc_stride_page = value_cache.stride(0);
+  a.vc_stride_page = page_tokens == 16 ? value_cache.stride(0) : 16 * value_cache.stride(1);
   a.vc_stride_token = value_cache.stride(1);
   a.vc_stride_head = value_cache.stride(2);
-  a.num_pages = key_cache.size(0);
+  a.num_pages = key_cache.size(0) * (page_tokens / 16);
   a.cache_dtype = fp8 ? L20_PD_KV_FP8_E4M3 : (key.scalar_type() == at::kBFloat16 ? L20_PD_KV_BF16 : L20_PD_KV_FP16);
   a.k_scale = 1.0f;
   a.v_scale = 1.0f;

@@ -33,6 +33,16 @@ Workspace = Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]
 Scale = Union[float, torch.Tensor]
 
 
+
+def _page_ok(key_cache: torch.Tensor, value_cache: torch.Tensor) -> bool:
+    """Pages of any multiple of 16 tokens (the reference's Triton path takes any page
+    size, ``integrations/vllm/l20_paged_split_kv.py:156,182-200``); above 16 the
+    kernels read a page as 16-token sub-pages, so its tokens must be contiguous."""
+    page = key_cache.shape[1]
+    if page < 16 or page % 16 or page > 4096:
+        return False
+    return page == 16 or all(c.stride(0) == page * c.stride(1) for c in (key_cache, value_cache))
+
 def _num_splits(max_seq_len: int, split_size: int) -> int:
     return max(1, math.ceil(max_seq_len / split_size)) if max_seq_len > 0 else 1
 
@@ -107,14 +117,14 @@ def l20_paged_split_kv_attention_fp8(
     if (
         head_dim not in (64, 128)
         or cache_dim != head_dim
-        or page_size != 16
+        or not _page_ok(key_cache, value_cache)
         or num_q_heads % num_kv_heads
         or q_len < 1
         or rows % q_len
         or block_table.shape[0] != batch
         or seq_lens.numel() != batch
     ):
-        raise RuntimeError("requires compatible head_dim=64/128, 16-token-page GQA tensors")
+        raise RuntimeError("requires compatible head_dim=64/128 GQA tensors with pages of a multiple of 16 tokens")
     if max_seq_len is None:
         max_seq_len = int(seq_lens.max().item())
     if split_size is None:
@@ -183,14 +193,14 @@ def l20_paged_split_kv_attention(
     if (
         head_dim not in (64, 128)
         or cache_dim != head_dim
-        or page_size != 16
+        or not _page_ok(key_cache, value_cache)
         or num_q_heads % num_kv_heads
         or q_len < 1
         or rows % q_len
         or block_table.shape[0] != batch
         or seq_lens.numel() != batch
     ):
-        raise RuntimeError("requires compatible head_dim=64/128, 16-token-page GQA tensors")
+        raise RuntimeError("requires compatible head_dim=64/128 GQA tensors with pages of a multiple of 16 tokens")
     if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
         raise RuntimeError("K/V cache must have the query's dtype (fp16 or bf16)")
     if max_seq_len is None:

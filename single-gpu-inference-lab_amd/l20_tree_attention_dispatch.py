@@ -52,7 +52,10 @@ def should_dispatch_l20_tree_attention(
         return False
     if query.shape[-1] not in (64, 128) or key_cache.shape[-1] != query.shape[-1]:
         return False
-    if key_cache.shape[1] != 16:
+    page = key_cache.shape[1]
+    if page < 16 or page % 16 or page > 4096:
+        return False
+    if page > 16 and key_cache.stride(0) != page * key_cache.stride(1):
         return False
     if query.shape[0] != block_table.shape[0]:
         return False

@@ -128,9 +128,11 @@ def _check_common(query: torch.Tensor, key_cache: torch.Tensor, value_cache: tor
     if not is_mi355x(query.device):
         raise RuntimeError("requires an MI355X (gfx950) GPU")
     if key_cache.ndim != 4 or value_cache.shape != key_cache.shape:
-        raise ValueError("expected key/value cache=[pages,16,Hkv,D]")
-    if key_cache.shape[1] != 16:
-        raise ValueError("paged tree attention requires page_size=16")
+        raise ValueError("expected key/value cache=[pages,page,Hkv,D]")
+    page = key_cache.shape[1]
+    if page < 16 or page % 16 or page > 4096 or (
+            page > 16 and any(c.stride(0) != page * c.stride(1) for c in (key_cache, value_cache))):
+        raise ValueError("paged tree attention requires pages of a multiple of 16 tokens, held contiguously")
     if query.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("query must be fp16 or bf16")
     if key_cache.dtype not in (torch.float8_e4m3fn, query.dtype) or value_cache.dtype != key_cache.dtype:

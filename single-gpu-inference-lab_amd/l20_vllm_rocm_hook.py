@@ -3,7 +3,7 @@
 The counterpart of the decode branch that the reference injects into vLLM's
 CUDA FlashInfer backend (``integrations/vllm/install_l20_fp8_paged_decode.py:63-149``,
 paths relative to the reference repo root).  On ROCm the NHD paged cache
-(``[num_blocks, 16, num_kv_heads, head_size]``) lives in vLLM's Triton attention
+(``[num_blocks, block_size, num_kv_heads, head_size]``) lives in vLLM's Triton attention
 backend (``vllm/v1/attention/backends/triton_attn.py``), whose forward calls
 ``unified_attention`` for every token; ``install_l20_fp8_paged_decode_rocm.py``
 inserts, right before that call::
@@ -21,8 +21,8 @@ reference's:
   being captured, the KV cache is fp8 (``kv_cache_dtype`` "fp8"/"fp8_e4m3" for
   OCP e4m3fn bytes or "fp8_e5m2" for e5m2 bytes -- the reference's hook takes every
   quantized cache, and vLLM's backend views both as its platform fp8 type, so the
-  op gets the bytes re-viewed in the setting's format) in 16-token
-  pages with head_size 64/128, the batch is pure decode (``max_query_len == 1``)
+  op gets the bytes re-viewed in the setting's format) in blocks of any
+  multiple of 16 tokens (vLLM's block size passes through) with head_size 64/128, the batch is pure decode (``max_query_len == 1``)
   and the layer uses none of ALiBi, sliding windows, logit soft-capping,
   attention sinks or a fused output quantisation (``output_scale`` given, or an
   output buffer whose dtype is not the query's);
@@ -110,7 +110,12 @@ def decode_gate(impl: Any, layer: Any, query: torch.Tensor, key_cache: torch.Ten
     if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
         return False
     _, block, kv_heads, head_size = key_cache.shape
-    if block != 16 or head_size not in (64, 128) or query.dim() != 3 or query.shape[-1] != head_size:
+    # vLLM's block size passes through: any multiple of 16 tokens whose rows
+    # are contiguous within the block (its NHD caches are)
+    if block < 16 or block % 16 or block > 4096 or head_size not in (64, 128) or query.dim() != 3 \
+            or query.shape[-1] != head_size:
+        return False
+    if block > 16 and any(c.stride(0) != block * c.stride(1) for c in (key_cache, value_cache)):
         return False
     q_heads = query.shape[1]
     if q_heads % kv_heads or q_heads // kv_heads > 32:

@@ -48,15 +48,17 @@ def kv_format(cache) -> str:
 
 
 def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, device="cuda",
-                   dtype=torch.bfloat16, pool_extra=7, max_pages=None, garbage_tail=False, fp8="e4m3fn"):
+                   dtype=torch.bfloat16, pool_extra=7, max_pages=None, garbage_tail=False, fp8="e4m3fn",
+                   page=16):
     """Seeded paged inputs of an arbitrary shape (generated on CPU, copied to ``device``).
 
-    ``fp8`` picks the cache format: "e4m3fn" (the reference's quantiser) or "e5m2"."""
+    ``fp8`` picks the cache format: "e4m3fn" (the reference's quantiser) or "e5m2";
+    ``page`` the tokens per page (caches [pages, page, Hkv, D])."""
     import l20_pd_workloads as wl
 
     g = torch.Generator().manual_seed(seed)
     lens = torch.as_tensor(lens, dtype=torch.int32)
-    pages_per = (lens.to(torch.int64) + 15) // 16
+    pages_per = (lens.to(torch.int64) + page - 1) // page
     pool = int(pages_per.sum()) + pool_extra
     perm = torch.randperm(pool, generator=g).to(torch.int32)
     mp = max(1, int(pages_per.max())) if max_pages is None else max_pages
@@ -69,7 +71,7 @@ def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, 
     query = torch.randn(batch * q_len, hq, d, generator=g).to(dtype)
     caches = []
     for _ in range(2):
-        raw = torch.randn(pool, 16, hkv, d, generator=g).to(torch.bfloat16)
+        raw = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16)
         if fp8 == "e5m2":
             codes, scale = quantize_e5m2(raw, per_head_axis=2 if per_head else None)
         else:
@@ -79,8 +81,8 @@ def make_synthetic(batch, hq, hkv, d, lens, *, q_len=1, per_head=False, seed=0, 
             u8 = codes.view(torch.uint8)
             for b in range(batch):
                 L = int(lens[b])
-                if L % 16:
-                    u8[int(table[b, L // 16]), L % 16:] = 0x7F
+                if L % page:
+                    u8[int(table[b, L // page]), L % page:] = 0x7F
         caches.append((codes, scale))
     (kc, ks), (vc, vs) = caches
     return {
@@ -192,13 +194,13 @@ def compare(out, lse, exp_out, exp_lse, rows: Optional[np.ndarray] = None, check
 
 # ------------------------------------------------------------ 16-bit caches, CSR page lists
 def make_synthetic16(batch, hq, hkv, d, lens, *, dtype=torch.float16, q_len=1, seed=0, device="cuda",
-                     pool_extra=7, garbage_tail=False, csr_pad=0):
+                     pool_extra=7, garbage_tail=False, csr_pad=0, page=16):
     """Seeded inputs for the fp16/bf16-KV siblings: query and caches of ``dtype``, a
     block table and the same pages as a CSR list (``csr_pad`` garbage entries after
     each row, so that offsets and not row lengths are exercised)."""
     g = torch.Generator().manual_seed(seed)
     lens = torch.as_tensor(lens, dtype=torch.int32)
-    pages_per = (lens.to(torch.int64) + 15) // 16
+    pages_per = (lens.to(torch.int64) + page - 1) // page
     pool = int(pages_per.sum()) + pool_extra
     perm = torch.randperm(pool, generator=g).to(torch.int32)
     mp = max(1, int(pages_per.max()))
@@ -214,14 +216,14 @@ def make_synthetic16(batch, hq, hkv, d, lens, *, dtype=torch.float16, q_len=1, s
         indptr.append(indptr[-1] + n + csr_pad)
         off += n
     query = torch.randn(batch * q_len, hq, d, generator=g).to(dtype)
-    kc = torch.randn(pool, 16, hkv, d, generator=g).to(dtype)
-    vc = torch.randn(pool, 16, hkv, d, generator=g).to(dtype)
+    kc = torch.randn(pool, page, hkv, d, generator=g).to(dtype)
+    vc = torch.randn(pool, page, hkv, d, generator=g).to(dtype)
     if garbage_tail:
         for c in (kc, vc):
             for b in range(batch):
                 L = int(lens[b])
-                if L % 16:
-                    c[int(table[b, L // 16]), L % 16:] = float("nan")
+                if L % page:
+                    c[int(table[b, L // page]), L % page:] = float("nan")
     return {
         "query": query.to(device), "key_cache": kc.to(device), "value_cache": vc.to(device),
         "block_table": table.to(device), "seq_lens": lens.to(device),

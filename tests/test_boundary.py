@@ -130,7 +130,11 @@ BAD = [
     ("partial_splits", 3, "partial output workspace has wrong shape"),
     ("partial_output", 0, "partial output workspace has wrong shape"),
     ("head_dim", 96, "NHD cache only"),
-    ("page_size", 32, "NHD cache only"),
+    ("page_size", 24, "page_size must be a multiple of 16 from 16 through 4096"),
+    ("page_size", 8, "page_size must be a multiple of 16 from 16 through 4096"),
+    ("page_size", 4112, "page_size must be a multiple of 16 from 16 through 4096"),
+    # 32-token pages whose page stride is that of 16-token pages: not contiguous
+    ("page_size", 32, "pages of more than 16 tokens must hold them contiguously"),
     ("query_dtype", cabi.L20_PD_FP32, "query must be bf16 or fp16"),
     ("q_len", 0, "q_len must be >= 1"),
     ("q_len", 5, "GQA group x q_len must be at most 32"),
@@ -153,6 +157,18 @@ def test_check_rejects_bad_arguments(field, value, message):
     lib = cabi.load()
     assert lib.l20_pd_fp8_e4m3_split_out(ctypes.byref(a), None) == cabi.L20_PD_EINVAL
     assert message in cabi.last_error(lib)
+
+
+def test_check_accepts_pages_of_a_multiple_of_16_tokens():
+    # 64-token pages, contiguous: the block table then needs a quarter of the entries
+    a = valid_args()
+    a.page_size = 64
+    a.k_stride_page = a.v_stride_page = 64 * 4 * 128
+    a.bt_max_pages = 16
+    cabi.check(a)
+    a.bt_max_pages = 15  # 960 tokens < max_seq_len 1024
+    with pytest.raises(RuntimeError, match="block table has fewer pages than max_seq_len needs"):
+        cabi.check(a)
 
 
 def test_check_rejects_pair_count_beyond_int32():

@@ -161,6 +161,37 @@ def test_rope_and_cache_bit_exact(spec, dtype, cs_dtype, cache):
         np.testing.assert_array_equal(_np(vc), want_vc)
 
 
+@pytest.mark.parametrize("page", [32, 48])
+def test_rope_and_cache_pages_of_a_multiple_of_16_tokens(page):
+    """Caches of page-token blocks (vLLM's block size passes through): slot s is
+    row s % page of block s // page, bit-exact against the oracle."""
+    from oracle import kv_write_ref as kw
+    import l20_rope_kv
+
+    T, hq, hkv, d, rot = 37, 8, 2, 128, 128
+    c = _case(T, hq, hkv, d, rot, torch.bfloat16, torch.bfloat16, seed=page)
+    pages = (c["pages"] * 16 + page - 1) // page
+    kc = torch.zeros(pages, page, hkv, d, dtype=torch.float8_e4m3fn).cuda()
+    vc = torch.zeros_like(kc)
+    q, k, v = c["q"].cuda(), c["k"].cuda(), c["v"].cuda()
+    q_in, k_in = _np(q), _np(k)
+    l20_rope_kv.l20_rope_and_cache(q, k, v, c["pos"].cuda(), c["cs"].cuda(), True, kc, vc, c["slots"].cuda(),
+                                   k_scale=0.031, v_scale=0.017)
+    torch.cuda.synchronize()
+    kc0 = np.zeros(kc.shape, np.uint8)
+    want_q, want_k, want_kc, want_vc = kw.rope_and_cache(
+        q_in, k_in, _np(v), c["pos"].numpy(), _np(c["cs"]), True, kc0, kc0.copy(), c["slots"].numpy(),
+        dtype="bf16", cache_fp8=True, k_scale=0.031, v_scale=0.017)
+    np.testing.assert_array_equal(_np(q), want_q)
+    np.testing.assert_array_equal(kc.view(torch.uint8).cpu().numpy(), want_kc)
+    np.testing.assert_array_equal(vc.view(torch.uint8).cpu().numpy(), want_vc)
+    # padded blocks (block stride != page token strides) are refused
+    padded = torch.zeros(pages, page + 16, hkv, d, dtype=torch.float8_e4m3fn).cuda()[:, :page]
+    with pytest.raises(RuntimeError, match="contiguously"):
+        l20_rope_kv.l20_rope_and_cache(None, k, v, c["pos"].cuda(), c["cs"].cuda(), True, padded, padded,
+                                       c["slots"].cuda(), k_scale=0.031, v_scale=0.017)
+
+
 def test_rope_and_cache_rows_only_8_byte_aligned():
     """Q/K/V rows 8-byte but not 16-byte aligned (views at an offset of four
     elements) take the general path and give the same bytes."""

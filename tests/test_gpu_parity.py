@@ -125,6 +125,69 @@ def test_edge_cases(case, split):
     H.compare(*H.run_op(inp, split), *exp)
 
 
+# ------------------------------------------------------------ pages of 16 m tokens
+PAGED = [
+    # name, batch, hq, hkv, d, lens, q_len, per_head
+    ("ragged", 5, 28, 4, 128, [1, 100, 333, 1024, 47], 1, True),
+    ("empty_and_short", 4, 16, 2, 64, [0, 15, 16, 65], 1, False),
+    ("verify_q4", 3, 16, 2, 128, [70, 4, 2049], 4, False),
+]
+
+
+@pytest.mark.parametrize("case", PAGED, ids=[c[0] for c in PAGED])
+@pytest.mark.parametrize("page", [32, 48, 64])
+@pytest.mark.parametrize("split", [64, 256, 1024])
+def test_pages_of_a_multiple_of_16_tokens(case, page, split):
+    """Caches of page-token pages (the reference hook's ``token // page_size``
+    gather, integrations/vllm/l20_paged_split_kv.py:182-200), bytes past each
+    sequence's end NaN: the torch op and the C ABI against the oracle."""
+    name, batch, hq, hkv, d, lens, q_len, per_head = case
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, per_head=per_head, page=page,
+                           seed=zlib.crc32(name.encode()) % 1000 + page, garbage_tail=True)
+    assert inp["key_cache"].shape[1] == page
+    exp = H.run_oracle(inp)
+    H.compare(*H.run_op(inp, split, via="torch"), *exp)
+    H.compare(*H.run_op(inp, split, via="cabi", partial_dtype=torch.float16), *exp)
+
+
+@pytest.mark.parametrize("csr", [False, True], ids=["table", "csr"])
+@pytest.mark.parametrize("page", [32, 64])
+def test_16bit_kv_pages_of_a_multiple_of_16_tokens(csr, page):
+    inp = H.make_synthetic16(4, 16, 2, 128, [1, 300, 1000, 64], dtype=torch.bfloat16, seed=page, page=page,
+                             csr_pad=2, garbage_tail=True)
+    H.compare(*H.run_op16(inp, 256, csr=csr), *H.run_oracle16(inp, csr=csr))
+
+
+def test_hook_api_passes_the_block_size_through():
+    import l20_paged_split_kv as hook
+
+    inp = H.make_synthetic(3, 28, 4, 128, [900, 31, 2500], seed=8, page=64)
+    q = inp["query"]
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device)
+    hook.l20_paged_split_kv_attention_fp8(q, inp["key_cache"], inp["value_cache"], inp["block_table"],
+                                          inp["seq_lens"], output=out, k_scale=inp["k_scale"],
+                                          v_scale=inp["v_scale"], lse=lse)
+    H.compare(out, lse, *H.run_oracle(inp))
+    # every other token row of a wider buffer: still one token stride per page, read right
+    wide = torch.zeros(inp["key_cache"].shape[0], 128, 4, 128, dtype=torch.uint8, device=q.device)
+    wide[:, ::2] = inp["key_cache"].view(torch.uint8)
+    wide_v = torch.zeros_like(wide)
+    wide_v[:, ::2] = inp["value_cache"].view(torch.uint8)
+    out2 = torch.empty_like(q)
+    hook.l20_paged_split_kv_attention_fp8(q, wide[:, ::2].view(inp["key_cache"].dtype),
+                                          wide_v[:, ::2].view(inp["key_cache"].dtype), inp["block_table"],
+                                          inp["seq_lens"], output=out2, k_scale=inp["k_scale"],
+                                          v_scale=inp["v_scale"])
+    assert torch.equal(out2, out)
+    # padded pages (page stride != 64 token strides) are refused, not misread
+    padded = torch.zeros(inp["key_cache"].shape[0], 80, 4, 128, dtype=inp["key_cache"].dtype,
+                         device=q.device)[:, :64]
+    with pytest.raises(RuntimeError):
+        hook.l20_paged_split_kv_attention_fp8(q, padded, padded, inp["block_table"], inp["seq_lens"],
+                                              output=out, k_scale=inp["k_scale"], v_scale=inp["v_scale"])
+
+
 def test_c_abi_and_torch_op_agree_bitwise():
     inp = H.make_synthetic(3, 28, 4, 128, [900, 31, 4000], seed=5)
     a = H.run_op(inp, 256, via="torch")

@@ -213,6 +213,55 @@ def test_single_token_returns_v0_and_dominant_score_selects_its_row():
     np.testing.assert_allclose(out[0, 0], ref.e4m3fn_to_f32(vc[1, 3, 0]), rtol=1e-6)
 
 
+def _as_pages(case, page):
+    """The same logical tokens in ``page``-token pages: 16-token page ``j`` of a
+    sequence goes to row ``16 (j % m)`` of page ``table[b, j // m]`` (m = page / 16)
+    of a pool laid out afresh, with a permuted page order."""
+    m = page // 16
+    table16, kc16, vc16 = case["block_table"], case["key_cache"], case["value_cache"]
+    batch, n16 = table16.shape
+    n_p = (n16 + m - 1) // m
+    rng = np.random.default_rng(page)
+    perm = rng.permutation(batch * n_p + 2)
+    table = perm[:batch * n_p].reshape(batch, n_p).astype(np.int32)
+    shape = (batch * n_p + 2, page) + kc16.shape[2:]
+    kc = np.zeros(shape, dtype=kc16.dtype)
+    vc = np.zeros(shape, dtype=vc16.dtype)
+    for b in range(batch):
+        for j in range(n16):
+            kc[table[b, j // m], 16 * (j % m):16 * (j % m) + 16] = kc16[table16[b, j]]
+            vc[table[b, j // m], 16 * (j % m):16 * (j % m) + 16] = vc16[table16[b, j]]
+    return dict(case, key_cache=kc, value_cache=vc, block_table=table)
+
+
+@pytest.mark.parametrize("page", [32, 64, 48])
+@pytest.mark.parametrize("spec", [dict(seed=11, batch=2, hq=4, hkv=2, d=64, lens=[70, 33]),
+                                  dict(seed=12, batch=2, hq=4, hkv=2, d=64, lens=[45, 96], q_len=3)])
+def test_pages_of_any_multiple_of_16_tokens(spec, page):
+    """Pages of P tokens (the reference hook's ``token // page_size``, ``token %
+    page_size`` gather, integrations/vllm/l20_paged_split_kv.py:182-200): the same
+    logical tokens give bitwise the 16-token-page answer, and the fp64 loop agrees."""
+    case16 = make_case(**spec)
+    case = _as_pages(case16, page)
+    out, lse = run(ref.reference, case)
+    out16, lse16 = run(ref.reference, case16)
+    assert np.array_equal(out, out16) and np.array_equal(lse, lse16)
+    out64, lse64 = run(ref.brute_force_fp64, case)
+    np.testing.assert_allclose(out, out64, atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(lse, lse64, atol=2e-6, rtol=1e-6)
+    # The kernels' view: the cache as 16-token sub-pages, tile j of a sequence at
+    # sub-page table[b, j // m] * m + j % m -- bitwise the same answer; without the
+    # sub-page term it reads other tokens.
+    m = page // 16
+    sub = dict(case, key_cache=case["key_cache"].reshape((-1, 16) + case["key_cache"].shape[2:]),
+               value_cache=case["value_cache"].reshape((-1, 16) + case["value_cache"].shape[2:]))
+    j = np.arange(case["block_table"].shape[1] * m)
+    out_sub, lse_sub = run(ref.reference, dict(sub, block_table=case["block_table"][:, j // m] * m + j % m))
+    assert np.array_equal(out_sub, out) and np.array_equal(lse_sub, lse)
+    out_wrong, _ = run(ref.reference, dict(sub, block_table=case["block_table"][:, j // m] * m))
+    assert not np.allclose(out_wrong, out, atol=1e-3)
+
+
 def test_reference_masked_attention_known_answer():
     """tests/test_tree_attention.py:36-53 of the reference, restated for the chain mask.
 

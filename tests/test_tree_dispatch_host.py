@@ -42,7 +42,10 @@ def test_tree_gate_truth_table(on_mi355x, monkeypatch):
     assert not d.should_dispatch_l20_tree_attention(*_call(d_head=96))
     assert not d.should_dispatch_l20_tree_attention(*_call(kv_dtype=torch.float16))  # cache dtype != query dtype
     assert not d.should_dispatch_l20_tree_attention(*_call(kv_dtype=torch.float8_e4m3fn))
-    assert not d.should_dispatch_l20_tree_attention(*_call(page=32))
+    assert d.should_dispatch_l20_tree_attention(*_call(page=32))           # pages of any multiple of 16 tokens
+    assert d.should_dispatch_l20_tree_attention(*_call(page=64))
+    assert not d.should_dispatch_l20_tree_attention(*_call(page=24))
+    assert not d.should_dispatch_l20_tree_attention(*_call(page=8))
     assert not d.should_dispatch_l20_tree_attention(*_call(suffix_draft=3))
     q, kc, sk, bt, n = _call()
     assert not d.should_dispatch_l20_tree_attention(q, kc, sk, bt[:1], n)  # batch mismatch
