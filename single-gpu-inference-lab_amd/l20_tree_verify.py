@@ -36,6 +36,7 @@ dtype; head_dim 64 or 128; 16-token pages.
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Optional, Tuple, Union
 
 import torch
@@ -235,6 +236,36 @@ def allocate_tree_attention_workspace(query: torch.Tensor) -> TreeAttentionWorks
          torch.empty((*summary, head_dim), **f32), torch.empty(summary, **f32), torch.empty(summary, **f32)))
 
 
+# Six-tensor tuples given as workspaces keep the extra buffers of their wrapper
+# across calls: id of the first tensor -> (weak reference to it, the buffer
+# dict).  Only the buffers are held, never the caller's tensors, and the entry
+# goes when that tensor does.
+_WRAPPED = {}
+
+
+def _as_workspace(workspace, query: torch.Tensor) -> TreeAttentionWorkspace:
+    """``workspace`` as a TreeAttentionWorkspace: None allocates one, a
+    TreeAttentionWorkspace is used as is, the reference's six-tensor tuple
+    (``triton_tree_attention.py:761-776``) is wrapped; anything else is refused
+    rather than silently replaced by a fresh allocation."""
+    if workspace is None:
+        return allocate_tree_attention_workspace(query)
+    if isinstance(workspace, TreeAttentionWorkspace):
+        return workspace
+    if isinstance(workspace, (tuple, list)) and len(workspace) == 6 and all(
+            isinstance(t, torch.Tensor) for t in workspace):
+        first = workspace[0]
+        entry = _WRAPPED.get(id(first))
+        if entry is None or entry[0]() is not first:
+            entry = (weakref.ref(first), {})
+            _WRAPPED[id(first)] = entry
+            weakref.finalize(first, _WRAPPED.pop, id(first), None)
+        ws = TreeAttentionWorkspace(tuple(workspace))
+        ws._buffers = entry[1]
+        return ws
+    raise TypeError("workspace must come from allocate_tree_attention_workspace (or be its six-tensor tuple)")
+
+
 def _check_block_t(block_t: Optional[int]) -> None:
     # The reference's Triton tile knob (triton_tree_attention.py:1071-1074); the
     # HIP kernel's tiling is fixed, so it is only validated.
@@ -265,11 +296,18 @@ def hybrid_tree_attention_paged_prefix(
     """Tree attention over a paged prefix of ``cached_length`` tokens plus a contiguous
     draft suffix (``triton_tree_attention.py:1040-1197``).
 
-    query [B, S, Hq, D]; key/value_cache [pages, 16, Hkv, D]; suffix_key/value
-    [B, S, Hkv, D] (query dtype); block_table [B, pages] covering cached_length
-    (with ``contiguous_pages`` the pages of sequence b are ``page_base[b] + t // 16``
-    instead, as in the reference); ancestor_mask [S, S] bool on the query's device.
-    Returns [B, S, Hq, D] in the query dtype (``output`` when given).
+    query [B, S, Hq, D]; key/value_cache [pages, P, Hkv, D] (P a multiple of 16);
+    suffix_key/value [B, S, Hkv, D] (query dtype); block_table [B, pages] covering
+    cached_length (with ``contiguous_pages`` the pages of sequence b are
+    ``page_base[b] + t // P`` instead, as in the reference); ancestor_mask [S, S] bool
+    on the query's device.  Returns [B, S, Hq, D] in the query dtype (``output`` when
+    given).  ``workspace`` is one from ``allocate_tree_attention_workspace`` or the
+    reference's six-tensor tuple (wrapped once and kept with the tuple).
+
+    Precision: the prefix pass writes its normalised output in the query dtype
+    (the decode op's output type) before the fp32 LSE merge with the suffix, so
+    the prefix share of each row is rounded twice (query dtype, then the final
+    output): at most one extra half-ulp of bf16 (2^-9 relative) on that share.
 
     Two launches of the HIP library: the prefix pass (the split-KV kernel with every
     draft row a query column, LSE out) and ``l20_pd_tree_suffix_merge`` (suffix
@@ -291,7 +329,8 @@ def hybrid_tree_attention_paged_prefix(
         raise ValueError("suffix KV must match query batch/draft and cache kv heads")
     if suffix_key.dtype != query.dtype or suffix_value.dtype != query.dtype:
         raise ValueError("suffix key/value must have the query's dtype")
-    if block_table.shape[0] != batch or block_table.shape[1] * 16 < cached_length:
+    page = key_cache.shape[1]  # tokens per page (a multiple of 16)
+    if block_table.shape[0] != batch or block_table.shape[1] * page < cached_length:
         raise ValueError("block_table does not cover cached_length")
     if ancestor_mask.shape != (draft, draft):
         raise ValueError("ancestor_mask must match draft_length")
@@ -304,7 +343,7 @@ def hybrid_tree_attention_paged_prefix(
         if page_base.ndim != 1 or page_base.shape[0] != batch:
             raise ValueError("page_base must have shape [B]")
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
-    ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
+    ws = _as_workspace(workspace, query)
     dev = query.device
     if output is None:
         output = torch.empty_like(query)
@@ -326,7 +365,7 @@ def hybrid_tree_attention_paged_prefix(
         if padded != draft:
             qb[:, draft:].zero_()
         rows_q = qb.view(entries * cols, num_q_heads, head_dim)
-    pages = max(1, math.ceil(cached_length / 16))
+    pages = max(1, math.ceil(cached_length / page))
     if contiguous_pages:
         ramp = ws.constant("ramp", lambda: torch.arange(pages, dtype=torch.int32, device=dev), (pages,), dev)
         table = ws.buffer("table", (entries, pages), torch.int32, dev)
@@ -384,7 +423,7 @@ def causal_verifier_attention_paged(
     draft = query.shape[1]
     if draft < 1 or draft > MAX_DRAFT:
         raise ValueError("causal verifier path supports draft_length in [1, 64]")
-    ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
+    ws = _as_workspace(workspace, query)
     chain = ws.constant("chain_mask", lambda: make_chain_tree_mask(draft, device=query.device), (draft, draft),
                         query.device)
     return hybrid_tree_attention_paged_prefix(
@@ -467,5 +506,5 @@ def hybrid_tree_attention_split(query: torch.Tensor, key: torch.Tensor, value: t
     of ``hybrid_tree_attention``; a ``TreeAttentionWorkspace`` keeps its buffers
     between calls."""
     _check_block_t(block_t)
-    ws = workspace if isinstance(workspace, TreeAttentionWorkspace) else allocate_tree_attention_workspace(query)
+    ws = _as_workspace(workspace, query)
     return _contiguous_tree(query, key, value, ancestor_mask, cached_length, ws, block_t, softmax_scale, output)

@@ -273,3 +273,53 @@ def run_oracle16(inp, rows: Optional[Sequence[int]] = None, csr=False):
         inp["value_cache"].float().cpu().numpy(), table.cpu().numpy(), inp["seq_lens"].cpu().numpy(),
         softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], rows=rows,
         page_indptr=inp["page_indptr"].cpu().numpy() if csr else None, tree_mask=_host_tree(inp))
+
+
+# ------------------------------------------------------------ tree attention oracles
+def dense_tree_oracle(query, prefix_k, prefix_v, suffix_k, suffix_v, mask, scale):
+    """fp64 attention over concat(prefix, suffix) keys: every row sees the prefix,
+    row i sees draft j iff mask[i, j] (any draft count, unlike the 32-bit words)."""
+    b, s, hq, d = query.shape
+    hkv = prefix_k.shape[2]
+    g = hq // hkv
+    p = prefix_k.shape[1]
+    visible = np.concatenate([np.ones((s, p), dtype=bool), mask], 1)  # [S, P+S]
+    out = np.zeros((b, s, hq, d))
+    for i in range(b):
+        keys = np.concatenate([prefix_k[i], suffix_k[i]], 0).astype(np.float64)
+        vals = np.concatenate([prefix_v[i], suffix_v[i]], 0).astype(np.float64)
+        q = query[i].astype(np.float64).reshape(s, hkv, g, d)
+        sc = np.einsum("ihgd,thd->ihgt", q, keys) * scale
+        sc = np.where(visible[:, None, None, :], sc, -np.inf)
+        w = np.exp(sc - sc.max(-1, keepdims=True))
+        w /= w.sum(-1, keepdims=True)
+        out[i] = np.einsum("ihgt,thd->ihgd", w, vals).reshape(s, hq, d)
+    return out
+
+
+def paged_tree_oracle(query, prefix_k, prefix_v, suffix_k, suffix_v, mask, scale, page=16):
+    """The pinned oracle (``oracle.paged_fp8_decode_ref.reference_dense_kv`` with tree
+    words) over the prefix keys followed by the draft keys, laid out as ``page``-token
+    pages of one float32 cache: ``(out [B, S, Hq, D], lse [B, S, Hq])``.  With an
+    all-False ``mask`` the rows see the prefix alone (the prefix pass's LSE)."""
+    from oracle import paged_fp8_decode_ref as ref
+
+    b, s, hq, d = query.shape
+    hkv = prefix_k.shape[2]
+    cached = prefix_k.shape[1]
+    length = cached + s
+    per = max(1, -(-length // page))
+    table = np.arange(b * per, dtype=np.int32).reshape(b, per)[:, ::-1].copy()  # pages out of order
+    kc = np.zeros((b * per, page, hkv, d), np.float32)
+    vc = np.zeros_like(kc)
+    for i in range(b):
+        keys = np.concatenate([prefix_k[i], suffix_k[i]], 0)
+        vals = np.concatenate([prefix_v[i], suffix_v[i]], 0)
+        for t in range(length):
+            kc[table[i, t // page], t % page] = keys[t]
+            vc[table[i, t // page], t % page] = vals[t]
+    m = np.asarray(mask, dtype=bool)
+    words = (m.astype(np.int64) << np.arange(s, dtype=np.int64)).sum(1)  # row i: bit j iff mask[i, j]
+    out, lse = ref.reference_dense_kv(query.reshape(b * s, hq, d), kc, vc, table, np.full(b, length), q_len=s,
+                                      softmax_scale=scale, tree_mask=words)
+    return out.reshape(b, s, hq, d), lse.reshape(b, s, hq)

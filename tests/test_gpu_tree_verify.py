@@ -119,35 +119,17 @@ def test_tree_mask_rejects_bad_shapes():
 
 
 # ------------------------------------------------------------------ Python entry points
-def _dense_oracle(query, prefix_k, prefix_v, suffix_k, suffix_v, mask, scale):
-    """fp64 attention over concat(prefix, suffix) keys: every row sees the prefix,
-    row i sees draft j iff mask[i, j] (any draft count, unlike the 32-bit words)."""
-    b, s, hq, d = query.shape
-    hkv = prefix_k.shape[2]
-    g = hq // hkv
-    p = prefix_k.shape[1]
-    visible = np.concatenate([np.ones((s, p), dtype=bool), mask], 1)  # [S, P+S]
-    out = np.zeros((b, s, hq, d))
-    for i in range(b):
-        keys = np.concatenate([prefix_k[i], suffix_k[i]], 0).astype(np.float64)
-        vals = np.concatenate([prefix_v[i], suffix_v[i]], 0).astype(np.float64)
-        q = query[i].astype(np.float64).reshape(s, hkv, g, d)
-        sc = np.einsum("ihgd,thd->ihgt", q, keys) * scale
-        sc = np.where(visible[:, None, None, :], sc, -np.inf)
-        w = np.exp(sc - sc.max(-1, keepdims=True))
-        w /= w.sum(-1, keepdims=True)
-        out[i] = np.einsum("ihgt,thd->ihgd", w, vals).reshape(s, hq, d)
-    return out
+_dense_oracle = H.dense_tree_oracle  # pinned against the paged oracle in test_tree_oracle.py
 
 
-def _paged_prefix(batch, hkv, d, cached, kv_dtype, seed):
+def _paged_prefix(batch, hkv, d, cached, kv_dtype, seed, page=16):
     g = torch.Generator().manual_seed(seed)
-    pages = (cached + 15) // 16
+    pages = (cached + page - 1) // page
     pool = batch * pages + 3
     perm = torch.randperm(pool, generator=g).to(torch.int32)
     table = perm[: batch * pages].view(batch, pages).contiguous() if pages else torch.zeros(batch, 1, dtype=torch.int32)
-    raw_k = torch.randn(pool, 16, hkv, d, generator=g)
-    raw_v = torch.randn(pool, 16, hkv, d, generator=g)
+    raw_k = torch.randn(pool, page, hkv, d, generator=g)
+    raw_v = torch.randn(pool, page, hkv, d, generator=g)
     if kv_dtype == "fp8":
         import l20_pd_workloads as wl
 
@@ -168,37 +150,81 @@ def _paged_prefix(batch, hkv, d, cached, kv_dtype, seed):
 
 
 HYBRID = [
-    # batch, hq, hkv, d, cached, draft, kv
-    (2, 8, 2, 128, 1000, 4, "fp8"),
-    (2, 28, 4, 128, 2049, 8, "fp8"),      # 56 columns -> two packed chunks
-    (1, 8, 8, 128, 700, 40, torch.bfloat16),  # 40 drafts (suffix > 32) -> chunks of 32
-    (3, 16, 16, 64, 333, 5, torch.float16),
-    (2, 8, 2, 128, 0, 3, "fp8"),          # no cached prefix
+    # batch, hq, hkv, d, cached, draft, kv, page
+    (2, 8, 2, 128, 1000, 4, "fp8", 16),
+    (2, 28, 4, 128, 2049, 8, "fp8", 16),      # 56 columns -> two packed chunks
+    (1, 8, 8, 128, 700, 40, torch.bfloat16, 16),  # 40 drafts (suffix > 32) -> chunks of 32
+    (3, 16, 16, 64, 333, 5, torch.float16, 16),
+    (2, 8, 2, 128, 0, 3, "fp8", 16),          # no cached prefix
+    (2, 16, 4, 128, 1500, 6, "fp8", 32),      # 32-token pages
 ]
 
 
 @pytest.mark.parametrize("case", HYBRID, ids=[f"h{i}" for i in range(len(HYBRID))])
 def test_hybrid_tree_attention_paged_prefix(case):
+    """Output against the pinned paged oracle (max-abs and cosine; drafts beyond a
+    32-bit word against the dense restatement, pinned to it), and the prefix pass's
+    LSE (what the path computes as LSE) against the oracle's prefix-only LSE."""
     import l20_tree_verify as tv
 
-    batch, hq, hkv, d, cached, draft, kv = case
+    batch, hq, hkv, d, cached, draft, kv, page = case
     print(f"hybrid {case}", flush=True)
     qdt = torch.bfloat16 if kv in ("fp8", torch.bfloat16) else torch.float16
-    kc, vc, ks, vs, table, pk, pv = _paged_prefix(batch, hkv, d, cached, kv, seed=draft + cached)
+    kc, vc, ks, vs, table, pk, pv = _paged_prefix(batch, hkv, d, cached, kv, seed=draft + cached, page=page)
     g = torch.Generator().manual_seed(99 + draft)
     query = torch.randn(batch, draft, hq, d, generator=g).to(qdt)
     sk = torch.randn(batch, draft, hkv, d, generator=g).to(qdt)
     sv = torch.randn(batch, draft, hkv, d, generator=g).to(qdt)
     mask = random_tree(draft, np.random.default_rng(draft))
+    ws = tv.allocate_tree_attention_workspace(query.cuda())
     got = tv.hybrid_tree_attention_paged_prefix(
         query.cuda(), kc, vc, sk.cuda(), sv.cuda(), table, torch.from_numpy(mask).cuda(), cached,
-        k_scale=ks, v_scale=vs)
+        k_scale=ks, v_scale=vs, workspace=ws)
     torch.cuda.synchronize()
     assert got.shape == query.shape and got.dtype == qdt
-    exp = _dense_oracle(query.float().numpy(), pk, pv, sk.float().numpy(), sv.float().numpy(), mask, d ** -0.5)
-    g_np = got.float().cpu().numpy()
-    assert np.isfinite(g_np).all()
-    assert np.abs(g_np - exp).max() <= H.OUT_ATOL
+    args = (query.float().numpy(), pk, pv, sk.float().numpy(), sv.float().numpy())
+    if draft <= 32:
+        exp, _ = H.paged_tree_oracle(*args, mask, d ** -0.5)
+    else:
+        exp = _dense_oracle(*args, mask, d ** -0.5)
+    H.compare(got, None, exp, None, check_lse=False)
+    # the prefix pass's LSE: every draft row over the cached keys alone
+    p_lse = ws._buffers["prefix_lse"]
+    padded = p_lse.shape[0] // batch
+    got_lse = p_lse.view(batch, padded, hq)[:, :draft]
+    _, exp_lse = H.paged_tree_oracle(*args, np.zeros((draft, draft), dtype=bool), d ** -0.5)
+    if cached == 0:
+        assert torch.isneginf(got_lse).all()
+    else:
+        err = np.abs(got_lse.cpu().numpy() - exp_lse) / np.maximum(1.0, np.abs(exp_lse))
+        assert err.max() <= H.LSE_RTOL, float(err.max())
+
+
+def test_hybrid_accepts_the_reference_tuple_workspace():
+    """The reference's six-tensor workspace tuple is wrapped once and reused (its
+    buffers persist), and anything else is refused."""
+    import l20_tree_verify as tv
+
+    batch, hq, hkv, d, cached, draft = 2, 8, 2, 128, 600, 5
+    kc, vc, ks, vs, table, pk, pv = _paged_prefix(batch, hkv, d, cached, "fp8", seed=3)
+    g = torch.Generator().manual_seed(4)
+    query = torch.randn(batch, draft, hq, d, generator=g).to(torch.bfloat16).cuda()
+    sk = torch.randn(batch, draft, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    sv = torch.randn(batch, draft, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    mask = torch.from_numpy(random_tree(draft, np.random.default_rng(5))).cuda()
+    plain = tuple(tv.allocate_tree_attention_workspace(query))
+    a = tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, k_scale=ks, v_scale=vs,
+                                              workspace=plain)
+    wrapped = tv._as_workspace(plain, query)
+    before = {k: v.data_ptr() for k, v in wrapped._buffers.items()}
+    assert before, "the first call filled the wrapped workspace"
+    b = tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, k_scale=ks, v_scale=vs,
+                                              workspace=plain)
+    assert tv._as_workspace(plain, query)._buffers is wrapped._buffers
+    assert {k: v.data_ptr() for k, v in wrapped._buffers.items()} == before
+    assert torch.equal(a, b)
+    with pytest.raises(TypeError):
+        tv.hybrid_tree_attention_paged_prefix(query, kc, vc, sk, sv, table, mask, cached, workspace=plain[:3])
 
 
 def test_causal_verifier_equals_chain_hybrid_and_paged_tree():
@@ -414,7 +440,8 @@ CONTIG = [
 @pytest.mark.parametrize("case", CONTIG, ids=[f"c{i}" for i in range(len(CONTIG))])
 def test_contiguous_cache_tree_attention(case):
     """hybrid_tree_attention / hybrid_tree_attention_split (the reference's contiguous-cache
-    entry points, triton_tree_attention.py:706-886) against the fp64 dense oracle."""
+    entry points, triton_tree_attention.py:706-886) against the pinned paged oracle
+    (max-abs and cosine)."""
     import l20_tree_verify as tv
 
     batch, hq, hkv, d, cached, draft, dtype, layout = case
@@ -431,14 +458,14 @@ def test_contiguous_cache_tree_attention(case):
         value = torch.randn(batch, total, hkv, d, generator=g).to(dtype).cuda()
     mask = torch.from_numpy(random_tree(draft, np.random.default_rng(draft)))
     kf, vf = key.float().cpu().numpy(), value.float().cpu().numpy()
-    exp = _dense_oracle(query.float().numpy(), kf[:, :cached], vf[:, :cached], kf[:, cached:], vf[:, cached:],
-                        mask.numpy(), d ** -0.5)
+    exp, _ = H.paged_tree_oracle(query.float().numpy(), kf[:, :cached], vf[:, :cached], kf[:, cached:],
+                                 vf[:, cached:], mask.numpy(), d ** -0.5)
     a = tv.hybrid_tree_attention(query.cuda(), key, value, mask.cuda(), cached)
     ws = tv.allocate_tree_attention_workspace(query.cuda())
     b = tv.hybrid_tree_attention_split(query.cuda(), key, value, mask.cuda(), cached, workspace=ws, block_t=64)
     b2 = tv.hybrid_tree_attention_split(query.cuda(), key, value, mask.cuda(), cached, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(b, b2)
-    assert np.abs(a.float().cpu().numpy() - exp).max() <= H.OUT_ATOL
+    H.compare(a, None, exp, None, check_lse=False)
     with pytest.raises(ValueError, match="cached_length"):
         tv.hybrid_tree_attention(query.cuda(), key, value, mask.cuda(), cached + 1)
