@@ -226,15 +226,18 @@ def cpu_baseline_decode(inp, cfg, sample_seqs, elem_bytes, min_seconds=10.0):
     }
 
 
-def measured_traffic(workload: str, split: int, kernel: str = "pd_fp8_partial"):
+def measured_traffic(workload: str, split: int, kernel: str = "pd_fp8_partial", partial_dtype=None):
     """HBM bytes per launch of ``kernel`` from the committed counter profile
     (rocprofv3 FETCH_SIZE / WRITE_SIZE passes scaled by a copy of known size),
-    or None when the profile has no entry for this workload and split."""
+    or None when the profile has no entry for this workload, split and partial
+    workspace dtype."""
     path = ROOT / "profiles" / "hbm_traffic.json"
     if not path.exists():
         return None
     data = json.loads(path.read_text())
     for e in data["entries"]:
+        if partial_dtype is not None and e.get("partial_dtype", "fp32") != partial_dtype:
+            continue
         if e["workload"] == workload and e["split_size"] == split and e["kernel"] == kernel:
             read = e["fetch_kib"] * 1024 * data["fetch_scale"]
             write = e["write_kib"] * 1024 * data["write_scale"]
@@ -422,7 +425,7 @@ def run_decode(args, mode):
         cpu = cpu_baseline_decode(first, cfg, sample, elem)
 
     workload = cfg.name + {"decode": "", "decode16": "+bf16kv", "tree": "+tree"}[mode]
-    traffic = measured_traffic(workload, split)
+    traffic = measured_traffic(workload, split, partial_dtype=args.partial_dtype)
     line = {
         "metric": METRICS[mode],
         "value": round(value, 2),
