@@ -1074,20 +1074,25 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   const int hpw = p.num_kv_heads / nwaves;  // units per item and wave
   const bool compact = p.compact != 0;
   // Items beyond the split-major slots of the grid go through the queue.
-  // Then, in compact mode, only workgroups [0, G1) start on a split-major
-  // slot: split 0 of sequence w, at most one per CU (the first workgroup
-  // dispatched to each), so the static round has no holes; workgroup
-  // w >= G1 starts on queue item w - G1 of the compact numbering without a
-  // claim.  Its page ids need the LDS prefix first, but as the second
-  // workgroup on its CU its first loads would queue behind the first one's
-  // K/V burst anyway, and no queue item waits for a claim in the first round.
-  // (Config 3, B = 128 on a 512-workgroup grid: G1 = 128 rather than 256
-  // leaves 384 pre-assigned items, which most of its input sets fit, so their
-  // launches claim nothing: partial kernel 45.7 -> 45.4 us.)
+  // Then, in compact mode, only workgroups [0, G1), G1 = min(2B, G/2), start
+  // on a split-major slot -- one per CU, the first workgroup dispatched to
+  // each: split 0 of every sequence, then split 1 of sequences [0, G1 - B).
+  // Its page ids and length load together, so it needs no prefix.
+  // Workgroup w >= G1 starts on queue item w - G1 of the compact numbering
+  // without a claim.  Its page ids need the LDS prefix first, but as the
+  // second workgroup on its CU its first loads would queue behind the first
+  // one's K/V burst anyway.  A static slot that is a hole (split 1 of a
+  // one-split sequence) takes queue item G - G1 + its rank among the holes,
+  // again without a claim, so atomic claims number the items after those
+  // G - G1 + H (H holes) and are made only when the queue holds more.
+  // (Config 3, B = 128 on a 512-workgroup grid: every CU starts a static
+  // item at once, and most input sets need no claim: partial kernel 45.2 ->
+  // 44.3 us against split 0 alone as the static round, 45.7 with claims.)
   const bool queued = (int64_t)G < (int64_t)B * p.num_splits;
-  const int G1 = (compact && queued) ? min(B, (G + 1) / 2) : G;
+  const int G1 = (compact && queued) ? min(2 * B, (G + 1) / 2) : G;
   int *s_prefix = s_dyn;      // s_prefix[b]: queue items of sequences < b
   int *s_len = s_dyn + B + 1;  // clamped length of sequence b
+  int *s_holes = s_dyn + 2 * B + 1;  // static slots that are holes (split 1 of a one-split sequence)
 
   // ---- per-wave helpers ----
   auto n_blocks = [&](int s, int L) {
@@ -1209,7 +1214,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // before its first decode.
   auto build_prefix = [&]() {
     const int per = (B + 63) >> 6;  // sequences per lane, <= 64
-    int sum = 0;
+    int sum = 0, holes = 0;
     for (int e0 = 0; e0 < per; e0 += 8) {
       int lv[8];
 #pragma unroll
@@ -1224,9 +1229,13 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
           const int L = max(0, min(lv[e], p.l_cap));
           s_len[idx] = L;
           sum += max(0, splits_of_len(L, S) - static_splits(idx, G1, B));
+          holes += (idx < G1 - B && splits_of_len(L, S) <= 1) ? 1 : 0;
         }
       }
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) holes += __shfl_xor(holes, off);
+    if (lane == 0) s_holes[0] = holes;
     int incl = sum;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -1289,10 +1298,10 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // holds queue item blockIdx.x - G1 as if claimed; atomic claims number
   // the items after those)
   // claim: the counter's value before the atomic claim (item = its low half
-  // + G - G1), or for the pre-assigned item a negative low half vblk - G
-  // that maps to item vblk - G1 the same way (no flag: a boolean carried
-  // through the item loop cost the kernel ~60 SGPRs of spills).
-  uint64_t claim = vblk >= G1 ? (uint64_t)(uint32_t)(vblk - G) : 0u;
+  // + G - G1 + H), or for a pre-assigned item its number less 2^30, a
+  // negative low half (no flag: a boolean carried through the item loop
+  // cost the kernel ~60 SGPRs of spills).
+  uint64_t claim = vblk >= G1 ? (uint64_t)(uint32_t)(vblk - G1 - (1 << 30)) : 0u;
   bool claimed = vblk >= G1;
   // wave 0: the queue may still hold items (never, when the static round
   // covers every slot: then no workgroup claims)
@@ -1312,7 +1321,8 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
   // config 3 the claims' latency depends on where the counter line sits in
   // HBM (partial kernel 45.4-48.0 us over 64 positions), and most of its
   // input sets need no claim at all.
-  auto claims_needed = [&]() { return !compact || queue_total() > (int64_t)(G - G1); };
+  auto hole_count = [&]() { return compact ? lds_uniform(s_holes, 0) : 0; };
+  auto claims_needed = [&]() { return !compact || queue_total() > (int64_t)(G - G1) + hole_count(); };
   auto claim_point = [&]() {
     if (gwave == 0 && more && !claimed) {
       // without the prefix yet, resolve decides after its prefix wait
@@ -1350,6 +1360,18 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
         return;
       }
     }
+    if (!claimed && compact && t_item == 0 && cb == -2 && vblk < G1) {
+      // The static slot was a hole (split 1 of a one-split sequence): the
+      // hole takes pre-assigned queue item G - G1 + its rank among holes.
+      const int bh = vblk - B;
+      int h = 0;
+      for (int base = 0; base < bh; base += 64) {
+        const int idx = base + lane;
+        h += __popcll(__ballot(idx < bh && splits_of_len(s_len[idx], S) <= 1));
+      }
+      claim = (uint64_t)(uint32_t)((G - G1) + h - (1 << 30));
+      claimed = true;
+    }
     if (!claimed) {
       if (!claims_needed()) {
         more = false;
@@ -1362,7 +1384,7 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       const unsigned int lo = __builtin_amdgcn_readfirstlane((unsigned int)claim);
       const unsigned int hi = __builtin_amdgcn_readfirstlane((unsigned int)(claim >> 32));
       const bool atomic = (int)lo >= 0;
-      const int64_t c = (int64_t)(int)lo + (G - G1);
+      const int64_t c = atomic ? (int64_t)lo + (G - G1) + hole_count() : (int64_t)(int)lo + (1 << 30);
       claimed = false;
       // (c < 0: a counter left flagged for ~2^31 claims without a clear; its
       // low half now reads as a pre-assigned item)
@@ -1374,10 +1396,9 @@ __global__ __launch_bounds__(512) void pd_fp8_partial(PartialParams p) {
       if (c >= Q) {
         more = false;
         // The launch's last atomic claim: no other atomic on the counter
-        // follows.  Every workgroup stops at its first failure; those past
-        // the split-major round whose pre-assigned item fails make no atomic
-        // claim, and either way the last atomic returns Q + G - 1 (after the
-        // G - G1 offset; a pre-assigned failure is at most G - 1 - G1).
+        // follows.  When claims are made at all, every workgroup makes
+        // exactly one failing atomic claim (no pre-assigned item fails then),
+        // so the last atomic returns Q + G - 1 (after the G - G1 + H offset).
         if (atomic && lane == 0 && c == Q + G - 1) g_pd_queue[p.queue_slot][0] = 0ull;
         // A clean launch never claims past Q + G - 1 (a second check, for a
         // tag that happens to match).
@@ -2196,7 +2217,7 @@ hipError_t launch_partial(l20pd::PartialParams pp, int batch, int num_kv_heads, 
   pp.compact = partial_compact(batch) ? 1 : 0;
   pp.paired = partial_paired<QT, KT, D, NQT, TREE, NB>(num_kv_heads, nwaves, batch, pp.num_splits) ? 1 : 0;
   const int threads = 64 * nwaves * (pp.paired ? 2 : 1);
-  const size_t lds = pp.compact ? (size_t)(2 * batch + 1) * sizeof(int) : 0;
+  const size_t lds = pp.compact ? (size_t)(2 * batch + 2) * sizeof(int) : 0;
   const int64_t max_items = (int64_t)batch * pp.num_splits;
   // paired: each workgroup runs two virtual workgroups of the schedule
   const int grid = partial_grid<QT, KT, D, NQT, TREE, NB>(threads, lds, pp.paired ? (max_items + 1) / 2 : max_items);
