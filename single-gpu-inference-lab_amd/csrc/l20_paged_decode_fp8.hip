@@ -24,7 +24,7 @@
 //    A sequence with a single split writes the final output and LSE;
 //    otherwise the fp32 partial (O / l, m, l) goes to the caller's workspace.
 //
-//  pd_merge<QT, D, WPP, PK>   WPP waves per (query row, q head), WPP from the split
+//  pd_merge<QT, D, WPP, PK, SPEC>   WPP waves per (query row, q head), WPP from the split
 //    count; PK the partial element (0 fp32, 1 fp16, 2 bf16).  pd_merge_narrow<QT, D, PK>
 //    for at most eight splits and many pairs.
 //    LSE merge of a row's splits: M = max m_s, w_s = 2^(m_s - M) l_s,
@@ -1737,6 +1737,10 @@ struct MergeParams {
   int q_len, split_size, num_splits, po_kind;  // po_kind as in PartialParams
   int l_cap;  // same clamp as the partial kernel
   int rows, num_q_heads;
+  // Load every step of each wave's first step group before the split counts
+  // are known (a small workspace: reading slots past a row's count costs
+  // less than the round trip it saves).  Selects the kernel's SPEC instance.
+  int spec_all;
 };
 
 // WPP waves per (query row, q head) pair (WPP = 1, 2, 4, 8 or 16: enough
@@ -1745,7 +1749,7 @@ struct MergeParams {
 // a pair takes slots (w + WPP * step) * G + g, G = 512/D groups, so every load
 // of a wave is independent and issued together.  Each wave folds its groups
 // with shuffles; with WPP > 1 the pair's waves then combine through LDS.
-template <typename QT, int D, int WPP, int PK>
+template <typename QT, int D, int WPP, int PK, bool SPEC>
 __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams p) {
   constexpr int CH = D / 8;                // 8-dim chunks per row
   constexpr int SG = 64 / CH;              // slot groups per wave
@@ -1782,6 +1786,21 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
     l_pre = pl[(int64_t)sl * p.pl_ssplit];
     load_partial8_raw<PK>(p.po, base + (int64_t)sl * p.po_ssplit, r0_pre, r1_pre);
   }
+  // With SPEC (the host's spec_all), the first group's other steps load here
+  // as well.
+  constexpr int kSteps = 4;
+  float ms_pre[kSteps], ls_pre[kSteps];
+  i32x4 r0s_pre[kSteps], r1s_pre[kSteps];
+  if constexpr (SPEC) {
+#pragma unroll
+    for (int k = 1; k < kSteps; ++k) {
+      const int s = wp * SG + k * WPP * SG + g;
+      const int sl = s < p.num_splits ? s : 0;
+      ms_pre[k] = pm[(int64_t)sl * p.pm_ssplit];
+      ls_pre[k] = pl[(int64_t)sl * p.pl_ssplit];
+      load_partial8_raw<PK>(p.po, base + (int64_t)sl * p.po_ssplit, r0s_pre[k], r1s_pre[k]);
+    }
+  }
   int n = 0;
   if (live) {
     const int L = max(0, min(p.seq_lens[row / p.q_len], p.l_cap));
@@ -1805,7 +1824,6 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
   // nothing.  (Against a loop unrolled by two with the loads under the slot
   // test: call minus partial kernel 5.76 -> 5.57 us at config 3, 8.2 ->
   // 7.65 us at config 4.)
-  constexpr int kSteps = 4;
   auto fold = [&](int s, float m, float l, f32x4 a0, f32x4 a1) {
     if (s < n_here && m == m && m != -INFINITY) {
       const float m_new = fmaxf(mx, m);
@@ -1826,7 +1844,15 @@ __global__ __launch_bounds__(WPP > 4 ? 64 * WPP : 256) void pd_merge(MergeParams
     // the group's remaining steps load together, or (a row that the
     // preloaded step covers: a wave-uniform test) not at all
     const bool rest = !first || n_here > s0 + WPP * SG;
-    if (rest) {
+    if (SPEC && first) {
+#pragma unroll
+      for (int k = 1; k < kSteps; ++k) {
+        ms[k] = ms_pre[k];
+        ls[k] = ls_pre[k];
+        r0[k] = r0s_pre[k];
+        r1[k] = r1s_pre[k];
+      }
+    } else if (rest) {
 #pragma unroll
       for (int k = 0; k < kSteps; ++k) {
         if (k == 0 && first) continue;
@@ -2256,9 +2282,17 @@ hipError_t launch_merge_wpp(const l20pd::MergeParams &mp, int64_t pairs, hipStre
   constexpr int WPB = WPP > 4 ? WPP : 4;
   constexpr int PPB = WPB / WPP;
   const dim3 grid((unsigned)((pairs + PPB - 1) / PPB)), block(64 * WPB);
-  if (mp.po_kind == 0) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 0>), grid, block, 0, stream, mp);
-  else if (mp.po_kind == 1) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 1>), grid, block, 0, stream, mp);
-  else hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 2>), grid, block, 0, stream, mp);
+  // separate instances: a runtime test of spec_all cost 0.06 us per call at
+  // config 1, which never takes it
+  if (mp.spec_all) {
+    if (mp.po_kind == 0) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 0, true>), grid, block, 0, stream, mp);
+    else if (mp.po_kind == 1) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 1, true>), grid, block, 0, stream, mp);
+    else hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 2, true>), grid, block, 0, stream, mp);
+  } else {
+    if (mp.po_kind == 0) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 0, false>), grid, block, 0, stream, mp);
+    else if (mp.po_kind == 1) hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 1, false>), grid, block, 0, stream, mp);
+    else hipLaunchKernelGGL((l20pd::pd_merge<QT, D, WPP, 2, false>), grid, block, 0, stream, mp);
+  }
   return hipGetLastError();
 }
 
@@ -2469,6 +2503,14 @@ l20pd::MergeParams merge_params(const l20_pd_fp8_args &a, int num_splits) {
   mp.split_size = a.split_size;
   mp.num_splits = num_splits;
   mp.po_kind = a.partial_dtype == L20_PD_FP32 ? 0 : a.partial_dtype == L20_PD_FP16 ? 1 : 2;
+  // Speculative first-group loads when the whole workspace is small (<= 4 MB
+  // of o partials) and has slots past the first step: config 2 (2 MB) then
+  // merges in one round trip; config 3 (14.7 MB, most rows far below the
+  // workspace's split count) and config 1 (every slot in the first step) do not.
+  const int64_t po_bytes = (int64_t)a.batch * a.q_len * a.num_q_heads * num_splits * a.head_dim *
+                           (mp.po_kind == 0 ? 4 : 2);
+  const int first_step = merge_waves_per_pair(num_splits, a.head_dim) * (512 / a.head_dim);
+  mp.spec_all = po_bytes <= ((int64_t)4 << 20) && num_splits > first_step ? 1 : 0;
   mp.l_cap = length_cap(a, num_splits);
   mp.rows = a.batch * a.q_len;
   mp.num_q_heads = a.num_q_heads;

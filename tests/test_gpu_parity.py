@@ -246,6 +246,32 @@ def test_narrow_merge_ignores_stale_slots(d, lens, split, pdt, q_len):
     H.compare(out, lse, *H.run_oracle(inp))
 
 
+@pytest.mark.parametrize("pdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_speculative_merge_loads_ignore_slots_past_each_row(pdt):
+    """A small workspace with more slots than a wave's first step (here 30
+    slots of 128 tokens, two waves per pair) is merged with every slot of the
+    first step group loaded before the row's split count is known: slots
+    past a row's count hold NaN / +inf and must not count, for rows of one
+    split up to the whole workspace."""
+    import l20_pd_cabi as cabi
+
+    lens = [3840, 1, 129, 0, 1000, 3000, 257, 640]
+    inp = H.make_synthetic(len(lens), 16, 2, 128, lens, seed=77)
+    po, pm, ps = H.workspace(inp, 128, pdt)
+    assert po.shape[2] == 30
+    for t, v in ((po, float("nan")), (pm, float("inf")), (ps, float("nan"))):
+        t.fill_(v)
+    q = inp["query"]
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device)
+    args = cabi.args_from_tensors(q, inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
+                                  po, pm, ps, out, inp["k_scale"], inp["v_scale"], inp["max_seq_len"], 128,
+                                  softmax_scale=inp["softmax_scale"], lse=lse)
+    cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    H.compare(out, lse, *H.run_oracle(inp))
+
+
 def test_launches_on_two_streams_overlap_safely():
     """Two calls in flight on one device (two streams, each with its own
     workspace) use different work-queue counters: results are bitwise those
