@@ -204,6 +204,14 @@ int32_t l20_pd_device_errors(int32_t clear);
  * normally. */
 int32_t l20_pd_set_spin_limit(uint32_t polls);
 
+/* Sets every work-queue counter of the current device to `value` (after a
+ * device synchronize), as a launch that gave up mid-way or shared a slot with
+ * another leaves it.  A test hook with no reference counterpart: with a value
+ * that no clean launch produces (e.g. a low half of 2^30), the next call that
+ * claims queue items reports L20_PD_DEVERR_QUEUE_SHARED, and
+ * l20_pd_device_errors(1) zeroes the counters again. */
+int32_t l20_pd_set_queue_counters(uint64_t value);
+
 /* Allocation-free variant of l20_pd_fp8_e4m3_split_out (no counterpart in the
  * reference: for callers that cannot allocate device memory, such as code
  * under HIP graph capture, tight serving loops or harnesses that forbid

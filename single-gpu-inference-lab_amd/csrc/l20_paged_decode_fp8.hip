@@ -2680,6 +2680,21 @@ int32_t l20_pd_set_spin_limit(uint32_t polls) {
   return L20_PD_OK;
 }
 
+int32_t l20_pd_set_queue_counters(uint64_t value) {
+  g_last_error[0] = '\0';
+  unsigned long long words[l20pd::kQueueSlots][8] = {};
+  static_assert(sizeof(words) == sizeof(l20pd::g_pd_queue), "one word per counter line");
+  for (int sl = 0; sl < l20pd::kQueueSlots; ++sl) words[sl][0] = value;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess)
+    e = hipMemcpyToSymbol(HIP_SYMBOL(l20pd::g_pd_queue), words, sizeof(words), 0, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    snprintf(g_last_error, sizeof(g_last_error), "l20_pd_set_queue_counters: %s", hipGetErrorString(e));
+    return L20_PD_ELAUNCH;
+  }
+  return L20_PD_OK;
+}
+
 int32_t l20_pd_device_errors(int32_t clear) {
   g_last_error[0] = '\0';
   unsigned int err[l20pd::kQueueSlots];

@@ -31,6 +31,7 @@ EXPORTED = (
     "l20_pd_fp8_e4m3_split_out_noalloc",
     "l20_pd_device_errors",
     "l20_pd_set_spin_limit",
+    "l20_pd_set_queue_counters",
     "l20_pd_split_out",
     "l20_pd_fp8_e4m3_partial",
     "l20_pd_fp8_e4m3_merge",
@@ -138,6 +139,8 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     lib.l20_pd_device_errors.restype = _i32
     lib.l20_pd_set_spin_limit.argtypes = [ctypes.c_uint32]
     lib.l20_pd_set_spin_limit.restype = _i32
+    lib.l20_pd_set_queue_counters.argtypes = [ctypes.c_uint64]
+    lib.l20_pd_set_queue_counters.restype = _i32
     lib.l20_pd_default_split_size.argtypes = [_i32, _i32, _i32, _i32]
     lib.l20_pd_default_split_size.restype = _i32
     lib.l20_pd_fp8_e4m3_dequant_f32.argtypes = [_vp, _vp, _i64, _f32, _vp]
@@ -294,6 +297,15 @@ def set_spin_limit(polls: int, lib: Optional[ctypes.CDLL] = None) -> None:
     """``l20_pd_set_spin_limit`` (0 restores the default)."""
     lib = lib or load()
     if lib.l20_pd_set_spin_limit(int(polls)) != L20_PD_OK:
+        raise RuntimeError(last_error(lib))
+
+
+def set_queue_counters(value: int, lib: Optional[ctypes.CDLL] = None) -> None:
+    """``l20_pd_set_queue_counters``: every work-queue counter of the current
+    device set to ``value`` (a test hook; ``device_errors(clear=True)`` zeroes
+    them)."""
+    lib = lib or load()
+    if lib.l20_pd_set_queue_counters(int(value)) != L20_PD_OK:
         raise RuntimeError(last_error(lib))
 
 

@@ -75,6 +75,39 @@ def test_hand_off_waits_give_up_and_report(monkeypatch):
     assert cabi.device_errors() == 0
 
 
+@pytest.mark.parametrize("value", [1 << 30, (0xDEADBEEF << 32) | 7])
+def test_a_counter_left_in_use_is_reported_and_cleared(value, monkeypatch):
+    """A work-queue counter that a launch left non-zero (a give-up mid-way, or
+    two launches on one slot) is found by the next launch that claims: the
+    call reports L20_PD_DEVERR_QUEUE_SHARED instead of silently skipping
+    items, and after clearing the same call is exact again."""
+    import l20_pd_cabi as cabi
+
+    assert cabi.device_errors(clear=True) == 0, "a device error was pending before this test"
+    lens = [1500 + 61 * i for i in range(24)]
+    inp = H.make_synthetic(24, 28, 4, 128, lens, seed=23)
+    exp = H.run_oracle(inp)
+    out = torch.empty_like(inp["query"])
+    lse = torch.empty(inp["query"].shape[:2], dtype=torch.float32, device="cuda")
+    # 5 workgroups for ~600 items: every launch claims from the counter
+    monkeypatch.setenv("L20_PD_MAX_WORKGROUPS", "5")
+    args = _call_args(inp, 256, out, lse)
+    cabi.set_queue_counters(value)
+    try:
+        cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert cabi.device_errors() == cabi.L20_PD_DEVERR_QUEUE_SHARED
+    finally:
+        cabi.device_errors(clear=True)
+    assert cabi.device_errors() == 0
+    out.zero_()
+    lse.zero_()
+    cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    H.compare(out, lse, *exp)
+    assert cabi.device_errors() == 0
+
+
 def test_graph_replays_interleaved_with_eager_launches_on_another_stream(monkeypatch):
     import l20_pd_cabi as cabi
 
