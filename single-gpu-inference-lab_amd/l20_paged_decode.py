@@ -69,6 +69,57 @@ def paged_decode_split_out(
     )
 
 
+def paged_decode_split(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    max_seq_len: int,
+    split_size: int,
+) -> torch.Tensor:
+    """Allocating form of ``paged_decode_split_out`` (the reference extension's
+    ``paged_decode_split``, ``l20_paged_decode.cu:511-547``, exported at
+    ``l20_paged_decode.cpp:147``): allocates the split workspace for
+    ``ceil(max_seq_len / split_size)`` splits, its o-partials in the query's
+    dtype as the reference does, and the output, and returns the output.  Every
+    call allocates; serving loops use the ``_out`` form with a reused workspace."""
+    if query.dim() != 3:
+        raise RuntimeError("invalid query")
+    batch, heads, dim = query.shape
+    splits = max(1, -(-int(max_seq_len) // int(split_size))) if int(split_size) > 0 else 1
+    partial_output = torch.empty(batch, heads, splits, dim, device=query.device, dtype=query.dtype)
+    partial_max = torch.empty(batch, heads, splits, device=query.device, dtype=torch.float32)
+    partial_sum = torch.empty_like(partial_max)
+    output = torch.empty_like(query)
+    return paged_decode_split_out(query, key_cache, value_cache, block_table, seq_lens, partial_output, partial_max,
+                                  partial_sum, output, max_seq_len, split_size)
+
+
+def paged_decode(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+) -> torch.Tensor:
+    """The reference extension's ``paged_decode`` (``l20_paged_decode.cu:467-494``,
+    exported at ``l20_paged_decode.cpp:146``): decode attention over fp16/bf16
+    paged caches with no length bound and no workspace argument, returning a
+    new output.  The reference runs one workgroup per (sequence, query head) over
+    the whole sequence; here the split kernel runs with the library's split size
+    for the longest sequence the block table holds (``block_table.size(1)``
+    pages of ``key_cache.size(1)`` tokens, known without reading ``seq_lens``
+    back from the device)."""
+    from l20_paged_split_kv import default_split_size
+
+    if query.dim() != 3 or key_cache.dim() != 4 or block_table.dim() != 2:
+        raise RuntimeError("Q must be [B,H,D], caches [pages,page_size,Hkv,D] and the block table [B,pages]")
+    max_seq_len = int(block_table.shape[1]) * int(key_cache.shape[1])
+    split = default_split_size(int(query.shape[0]), int(key_cache.shape[2]), max(1, max_seq_len), query.device)
+    return paged_decode_split(query, key_cache, value_cache, block_table, seq_lens, max_seq_len, split)
+
+
 def paged_decode_split_indices_out(
     query: torch.Tensor,
     key_cache: torch.Tensor,

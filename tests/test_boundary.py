@@ -244,6 +244,27 @@ def test_fake_impl_traces_under_fake_tensor_mode():
         assert out.shape == args[-1].shape
 
 
+def test_allocating_entry_points_of_the_reference_extension():
+    """The reference's extension module (l20_paged_decode.cpp:145-156) exports
+    paged_decode and paged_decode_split beside the three _out functions: this
+    module has all five names, and the allocating two return a new output of
+    the query's shape and dtype (here through the fake implementation, on meta
+    tensors, with the split size taken from the block table's bound)."""
+    import l20_paged_decode as ext
+
+    for name in ("paged_decode", "paged_decode_split", "paged_decode_split_out", "paged_decode_split_indices_out",
+                 "paged_decode_fp8_e4m3_split_out"):
+        assert callable(getattr(ext, name)), name
+    q = torch.empty(4, 16, 128, dtype=torch.float16, device="meta")
+    kc = torch.empty(64, 16, 8, 128, dtype=torch.float16, device="meta")
+    bt = torch.empty(4, 16, dtype=torch.int32, device="meta")
+    sl = torch.empty(4, dtype=torch.int32, device="meta")
+    for out in (ext.paged_decode(q, kc, kc, bt, sl), ext.paged_decode_split(q, kc, kc, bt, sl, 256, 64)):
+        assert out.shape == q.shape and out.dtype == q.dtype and out.device.type == "meta"
+    with pytest.raises(RuntimeError, match="invalid query"):
+        ext.paged_decode_split(q[0], kc, kc, bt, sl, 256, 64)
+
+
 def test_op_rejects_cpu_query_with_reference_message():
     import l20_paged_decode  # noqa: F401
 

@@ -550,6 +550,25 @@ def test_16bit_kv_reference_shapes(dtype, batch, ctx, csr):
     H.compare(*H.run_op16(inp, 512, csr=csr), *exp)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_allocating_entry_points_match_the_oracle(dtype):
+    """paged_decode and paged_decode_split, the reference extension's allocating
+    entry points (l20_paged_decode.cu:467-547), on its benchmark's head layout
+    (16 query heads, 8 KV heads, head_dim 128) with ragged lengths: each returns
+    a new output that matches the oracle; paged_decode takes its split size from
+    the block table's bound."""
+    import l20_paged_decode as ext
+
+    inp = H.make_synthetic16(4, 16, 8, 128, [512, 2048, 1, 700], dtype=dtype, seed=91)
+    exp_out, _ = H.run_oracle16(inp)
+    args = (inp["query"], inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"])
+    outs = [ext.paged_decode(*args)] + [ext.paged_decode_split(*args, inp["max_seq_len"], s) for s in (64, 128, 512)]
+    torch.cuda.synchronize()
+    for out in outs:
+        assert out.dtype == dtype and out.shape == inp["query"].shape
+        H.compare(out, None, exp_out, None)
+
+
 SIB_EDGE = [
     # name, batch, hq, hkv, d, lens, q_len
     ("ragged_d128", 5, 28, 4, 128, [1, 15, 16, 33, 1025], 1),
