@@ -202,12 +202,16 @@ def test_fp16_partial_workspace():
 
 
 @pytest.mark.parametrize("d,lens,split,pdt", [
-    (64, [8000, 3000, 1], 64, torch.float32),     # 125 splits: 8 waves per merged pair
-    (128, [6000, 0, 700], 64, torch.float16),     # 94 splits: 16 waves per pair, fp16 partials
-    (128, [2100, 1000], 160, torch.float32),      # 14 splits: 2 waves per pair
+    (64, [8000, 3000, 1], 64, torch.float32),     # 125 splits: 4 waves per merged pair
+    (128, [6000, 0, 700], 64, torch.float16),     # 94 splits: 8 waves per pair, fp16 partials
+    (128, [8300, 10, 4000], 64, torch.bfloat16),  # 130 splits: 16 waves per pair, bf16 partials
+    (128, [2100, 1000], 160, torch.float32),      # 14 splits: 1 wave per pair
 ])
 def test_merge_waves_per_pair(d, lens, split, pdt):
-    """The merge spreads a row's splits over 1-16 waves; every spread matches the oracle."""
+    """The merge spreads a row's splits over 1-16 waves (each wave takes up to
+    four steps of 512/D slots); every spread matches the oracle.  All four cases
+    also take the speculative first-group loads (workspaces under 4 MB with
+    slots past the first step)."""
     inp = H.make_synthetic(len(lens), 16, 2, d, lens, seed=split + d)
     H.compare(*H.run_op(inp, split, partial_dtype=pdt), *H.run_oracle(inp))
 
