@@ -333,6 +333,11 @@ def run_decode(args, mode):
         calls.append((a, (po, pm, ps, out, lse)))
     kvb = [wl.kv_bytes(s["seq_lens"], cfg.num_kv_heads, cfg.head_dim, elem) for s in sets]
     h = stream.cuda_stream
+    # Small batches of short sequences run as one launch (pd_fp8_fused, no
+    # merge): that kernel is then the call, and the roofline times it as such.
+    single = cabi.single_launch(calls[0][0], lib)
+    kernel = "pd_fp8_fused" if single else "pd_fp8_partial"
+    kernel_fn = cabi.split_out if single else cabi.partial
 
     settle_calls, settle_ms = settle(lambda i: cabi.split_out(calls[i % n_sets][0], h, lib), args.settle_ms)
     for i in range(args.warmup):
@@ -353,12 +358,12 @@ def run_decode(args, mode):
     ms_per_step = total_ms / args.steps
     # Timed region 2 (roofline): K partial launches back to back on the launch
     # stream between two events (the merge is not needed to time the partial
-    # kernel; every launch rewrites the same workspace).
+    # kernel; every launch rewrites the same workspace), or K single launches.
     p_start, p_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     p_start.record(stream)
     for k in range(args.steps):
-        cabi.partial(calls[k % n_sets][0], h, lib)
+        kernel_fn(calls[k % n_sets][0], h, lib)
     p_end.record(stream)
     torch.cuda.synchronize()
     partial_mean_ms = p_start.elapsed_time(p_end) / args.steps
@@ -368,9 +373,10 @@ def run_decode(args, mode):
     for k in range(args.steps):
         a = calls[k % n_sets][0]
         ev[k][0].record(stream)
-        cabi.partial(a, h, lib)
+        kernel_fn(a, h, lib)
         ev[k][1].record(stream)
-        cabi.merge(a, h, lib)
+        if not single:
+            cabi.merge(a, h, lib)
     torch.cuda.synchronize()
     partial_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
     # Region 4 (informational): the same K calls captured once into a HIP graph
@@ -425,7 +431,7 @@ def run_decode(args, mode):
         cpu = cpu_baseline_decode(first, cfg, sample, elem)
 
     workload = cfg.name + {"decode": "", "decode16": "+bf16kv", "tree": "+tree"}[mode]
-    traffic = measured_traffic(workload, split, partial_dtype=args.partial_dtype)
+    traffic = measured_traffic(workload, split, kernel=kernel, partial_dtype=None if single else args.partial_dtype)
     line = {
         "metric": METRICS[mode],
         "value": round(value, 2),
@@ -466,7 +472,7 @@ def run_decode(args, mode):
                 f"{n_sets * pool_bytes / 1e6:.0f} MB of K/V pools"),
             "parallelism": "single GPU",
         },
-        "roofline": roofline(achieved, "pd_fp8_partial", traffic, partial_ms, partial_mean_ms),
+        "roofline": roofline(achieved, kernel, traffic, partial_ms, partial_mean_ms),
         "cpu_baseline": cpu,
         "parity": check,
         "device": getattr(props, "gcnArchName", props.name),

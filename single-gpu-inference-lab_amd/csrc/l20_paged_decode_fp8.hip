@@ -1722,6 +1722,179 @@ __device__ __forceinline__ void unpack_partial8(i32x4 r0, i32x4 r1, f32x4 &a, f3
   }
 }
 
+// ---------------------------------------------------------------------------
+// Single-launch path for small batches
+// ---------------------------------------------------------------------------
+// One workgroup of kFusedWaves waves per (sequence, KV head) pair: wave w
+// streams the w-th of kFusedWaves equal token ranges of the sequence (a
+// multiple of 32 tokens, at most 1024: one page-id register) through the
+// partial kernel's per-unit math, NBF blocks in flight, and the waves'
+// online-softmax states meet in LDS, where every thread of the workgroup folds
+// them and writes output rows and LSE.  Nothing goes through the split
+// workspace and no merge kernel runs: for a batch whose pairs fit the CUs at
+// once this is the whole call (the host's fused_fits decides; l20_pd_single_launch
+// reports it).
+constexpr int kFusedWaves = 8;
+constexpr int kFusedMaxTokens = kFusedWaves * 1024;
+
+// Where finish_with puts a wave's normalised o row, running max and sum: the
+// fold's LDS slots, [wave][column][dim] and [wave][column] (the fields
+// finish_with reads, named as in PartialParams).
+struct FoldSlots {
+  int q_len, group, po_kind;
+  float *po;
+  int64_t po_srow, po_shead, po_ssplit;
+  float *pm;
+  int64_t pm_srow, pm_shead, pm_ssplit;
+  float *pl;
+  int64_t pl_srow, pl_shead, pl_ssplit;
+  void *out;
+  int64_t o_srow, o_shead;
+  float *lse;
+  int64_t lse_srow, lse_shead;
+};
+
+template <typename QT, int KT, int D, int NBF>
+__global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p) {
+  static_assert(KT != 1, "fp8 caches: 32-token blocks of two pages");
+  typedef KvUnit<QT, KT, D, 1, false, D == 128> U;
+  typedef typename U::Block Block;
+  typedef typename U::qvec8 qvec8;
+  __shared__ __attribute__((aligned(16))) char s_kx[U::kKLines ? kFusedWaves * U::kKxBytes : 16];
+  __shared__ __attribute__((aligned(16))) float s_o[kFusedWaves][16][D];
+  __shared__ float s_m[kFusedWaves][16], s_l[kFusedWaves][16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+  const int b = (int)(blockIdx.x / (unsigned)p.num_kv_heads);
+  const int kvh = (int)blockIdx.x - b * p.num_kv_heads;
+  char *const kx = s_kx + (U::kKLines ? wave * U::kKxBytes : 0);
+  const int q_len = p.q_len;
+  // (the host launches this kernel only when l_cap <= kFusedMaxTokens)
+  const int L = min(clamped_len(p, b), kFusedMaxTokens);
+  const int S = max(32, ((L + kFusedWaves - 1) / kFusedWaves + 31) & ~31);
+  const int start = wave * S;
+  const int uEnd = min(start + S, L);
+  const int tiles = max(0, (uEnd - start + kPage - 1) / kPage);
+  const int nU = (tiles + 1) >> 1;
+
+  // page ids of the wave's range: lane t -> tile t (-1 past the range, past
+  // the page list, and for an id outside the cache)
+  const int32_t *row = p.indptr ? p.bt + uniform_ld(p.indptr, b) : p.bt + (int64_t)b * p.bt_srow;
+  const int npages = p.indptr ? uniform_ld(p.indptr, b + 1) - uniform_ld(p.indptr, b) : p.bt_pages;
+  int pid = -1;
+  if (lane < tiles && lane < npages * p.page_mult - start / kPage) {
+    const int T = start / kPage + lane;
+    const int m = p.page_mult;
+    if (m == 1) {
+      const int e = row[T];
+      pid = (e >= 0 && (int64_t)e < p.num_pages) ? e : -1;
+    } else {
+      const int qq = (int)__umulhi((unsigned int)T, p.page_magic);  // T / m
+      const int e = row[qq];
+      const int64_t v = (int64_t)e * m + (T - qq * m);
+      pid = (e >= 0 && v < p.num_pages) ? (int)v : -1;
+    }
+  }
+  qvec8 qop[1][U::NS];
+  U::load_q(p, b, kvh, qop, n16, j);
+  const float k_scale = p.k_scale_ph ? uniform_ld(p.k_scale_ph, kvh) : p.k_scale;
+  const float v_scale = p.v_scale_ph ? uniform_ld(p.v_scale_ph, kvh) : p.v_scale;
+  const float c_log2 = k_scale * p.qk_scale_log2;
+  const int draft0 = L - q_len;
+  const int lim[1] = {min(uEnd - 1, draft0 + n16 % q_len)};
+  const int min_lim = min(uEnd - 1, draft0);
+  const int tree[1] = {0};
+
+  U st;
+  st.reset();
+  // block k lives in buf[k % NBF]; every buffer loads before the loop (a
+  // block past the range reads nothing: its page ids are -1)
+  Block buf[NBF];
+#pragma unroll
+  for (int i = 0; i < NBF; ++i) U::load_block(p, buf[i], pid, kvh, i, 3, n16, j);
+  // block k, then the refill of its buffer with block k + NBF: K as soon as
+  // the scores have consumed r.k, V after the block (the same loads on every
+  // path; past the range the page ids are -1)
+  auto step = [&](Block &r, int k) {
+    int pg[2] = {-1, -1};
+    if (k + NBF < nU) U::block_pages(pid, k + NBF, pg);
+    st.compute_block(r, pid, k, start + 32 * k, uEnd, draft0, lim, min_lim, tree, qop, c_log2, j, kx,
+                     [&]() { U::load_pages(p, r, pg, kvh, 1, n16, j); });
+    U::load_pages(p, r, pg, kvh, 2, n16, j);
+  };
+  int k = 0;
+  for (; k + NBF <= nU; k += NBF) {
+#pragma unroll
+    for (int i = 0; i < NBF; ++i) step(buf[i], k + i);
+  }
+#pragma unroll
+  for (int i = 0; i < NBF - 1; ++i)
+    if (k + i < nU) step(buf[i], k + i);
+
+  // every wave's (o / l, m, l) into its LDS slot: column 16 * 0 + n16 =
+  // g * q_len + i at [wave][column]
+  FoldSlots fs;
+  fs.q_len = q_len;
+  fs.group = p.group;
+  fs.po_kind = 0;
+  fs.po = &s_o[0][0][0];
+  fs.po_srow = D;
+  fs.po_shead = (int64_t)q_len * D;
+  fs.po_ssplit = 16 * D;
+  fs.pm = &s_m[0][0];
+  fs.pm_srow = 1;
+  fs.pm_shead = q_len;
+  fs.pm_ssplit = 16;
+  fs.pl = &s_l[0][0];
+  fs.pl_srow = 1;
+  fs.pl_shead = q_len;
+  fs.pl_ssplit = 16;
+  fs.out = nullptr;
+  fs.o_srow = fs.o_shead = 0;
+  fs.lse = nullptr;
+  fs.lse_srow = fs.lse_shead = 0;
+  st.finish_with(&fs, 0, 0, false, 0, wave, false, v_scale, n16, j, kx);
+  __syncthreads();
+
+  // fold: 4 dims of one column per thread and step
+  const int mcols = p.group * q_len;
+  constexpr int kQ = D / 4;
+  for (int idx = threadIdx.x; idx < mcols * kQ; idx += 64 * kFusedWaves) {
+    const int col = idx / kQ;
+    const int d0 = 4 * (idx - col * kQ);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kFusedWaves; ++w)
+      if (s_l[w][col] > 0.0f) mx = fmaxf(mx, s_m[w][col]);
+    float wsum = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kFusedWaves; ++w) {
+        const float l = s_l[w][col];
+        if (l > 0.0f) {
+          const float e = __builtin_amdgcn_exp2f(s_m[w][col] - mx) * l;
+          wsum += e;
+          acc += e * *reinterpret_cast<const f32x4 *>(&s_o[w][col][d0]);
+        }
+      }
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+    const int g = col / q_len;
+    const int i = col - g * q_len;
+    const int64_t orow = (int64_t)b * q_len + i;
+    const int64_t h = (int64_t)kvh * p.group + g;
+    QT *dst = reinterpret_cast<QT *>(p.out) + orow * p.o_srow + h * p.o_shead + d0;
+    *reinterpret_cast<i32x2 *>(dst) = i32x2{pack2<QT>(acc[0] * inv, acc[1] * inv), pack2<QT>(acc[2] * inv, acc[3] * inv)};
+    if (d0 == 0 && p.lse)
+      p.lse[orow * p.lse_srow + h * p.lse_shead] =
+          wsum > 0.0f ? kLn2 * (mx + __builtin_amdgcn_logf(wsum)) : -INFINITY;  // v_log_f32 is log2
+  }
+}
+
 struct MergeParams {
   const void *po;
   int64_t po_srow, po_shead, po_ssplit;
@@ -2277,6 +2450,43 @@ hipError_t launch_partial_shape(const l20pd::PartialParams &pp, int head_dim, in
                  : launch_partial_mask<QT, KT, false>(pp, head_dim, nqt, batch, num_kv_heads, stream);
 }
 
+// The single-launch kernel: one workgroup per (sequence, KV head), two blocks
+// in flight per wave.  (Three or four blocks spill at head_dim 128 -- 256
+// VGPRs and 44 / 284 bytes of scratch per lane -- and were slower on every
+// shape measured: config 1 5.81 / 5.83 / 6.05 us, 128 x 1024 tokens 15.2 /
+// 17.8 / 26.3 us for two / three / four.)
+constexpr int kFusedNB = 2;
+template <typename QT, int KT>
+hipError_t launch_fused(const l20pd::PartialParams &pp, int head_dim, int batch, int num_kv_heads,
+                        hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)batch * num_kv_heads)), block(64 * l20pd::kFusedWaves);
+  if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, kFusedNB>), grid, block, 0, stream, pp);
+  else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, kFusedNB>), grid, block, 0, stream, pp);
+  return hipGetLastError();
+}
+
+// Whether a call runs as the single launch: fp8 caches, one query tile (G x
+// q_len <= 16), no tree mask, at most one (sequence, KV head) pair per CU and
+// at most 1024 tokens per sequence the call may touch (four blocks per wave).
+// Then every pair streams at once on its own CU and the split workspace and
+// the merge launch are skipped.  Measured in one process against the split
+// kernels (per call): config 1 10.0 -> 5.8 us, 64 x 1024 tokens (2 KV heads)
+// 14.4 -> 12.2, 128 x 1024 20.4 -> 15.2; with eight blocks per wave and more
+// the pairs' CUs are latency-bound (each holds 8 waves x 2 blocks x 8 KB in
+// flight) and the split kernels win: config 2 (32 x 2048) 14.8 against 17.3,
+// 16 x 2048 13.0 against 16.8, 32 x 4096 19.3 against 28.4.
+// L20_PD_FUSED=0/1 overrides the size rule (tests and measurement; the shape
+// conditions and kFusedMaxTokens always hold).
+bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
+  if (kv16 || nqt != 1 || a.tree_mask) return false;
+  if (pp.l_cap > l20pd::kFusedMaxTokens) return false;
+  if (const char *env = getenv("L20_PD_FUSED")) return env[0] == '1';
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return (int64_t)a.batch * a.num_kv_heads <= cus && pp.l_cap <= 1024;
+}
+
 template <typename QT, int D, int WPP>
 hipError_t launch_merge_wpp(const l20pd::MergeParams &mp, int64_t pairs, hipStream_t stream) {
   constexpr int WPB = WPP > 4 ? WPP : 4;
@@ -2545,6 +2755,17 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   const bool bf16 = a->query_dtype == L20_PD_BF16;
   const int rows = a->batch * a->q_len;
   hipError_t e = hipSuccess;
+  if (stages == kBoth && fused_fits(*a, pp, nqt, kv16)) {
+    e = e5m2 ? (bf16 ? launch_fused<__bf16, 2>(pp, a->head_dim, a->batch, a->num_kv_heads, stream)
+                     : launch_fused<_Float16, 2>(pp, a->head_dim, a->batch, a->num_kv_heads, stream))
+             : (bf16 ? launch_fused<__bf16, 0>(pp, a->head_dim, a->batch, a->num_kv_heads, stream)
+                     : launch_fused<_Float16, 0>(pp, a->head_dim, a->batch, a->num_kv_heads, stream));
+    if (e != hipSuccess) {
+      snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
+      return L20_PD_ELAUNCH;
+    }
+    return L20_PD_OK;
+  }
   if (stages & kPartial) {
     const int D = a->head_dim, B = a->batch, H = a->num_kv_heads;
     if (kv16)
@@ -2678,6 +2899,18 @@ int32_t l20_pd_set_spin_limit(uint32_t polls) {
   }
   g_spin_limit[dev].store(polls ? polls : l20pd::kSpinLimit, std::memory_order_relaxed);
   return L20_PD_OK;
+}
+
+int32_t l20_pd_single_launch(const l20_pd_fp8_args *a) {
+  g_last_error[0] = '\0';
+  const int32_t rc = check_args(a);
+  if (rc != L20_PD_OK) return -rc;
+  if (a->batch == 0) return 0;
+  const bool kv16 = a->kv_dtype == L20_PD_KV_FP16 || a->kv_dtype == L20_PD_KV_BF16;
+  const int n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
+  const int nqt = (a->num_q_heads / a->num_kv_heads * a->q_len + 15) / 16;
+  const l20pd::PartialParams pp = partial_params(*a, n_s);
+  return fused_fits(*a, pp, nqt, kv16) ? 1 : 0;
 }
 
 int32_t l20_pd_set_queue_counters(uint64_t value) {

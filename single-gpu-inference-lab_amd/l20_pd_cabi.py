@@ -32,6 +32,7 @@ EXPORTED = (
     "l20_pd_device_errors",
     "l20_pd_set_spin_limit",
     "l20_pd_set_queue_counters",
+    "l20_pd_single_launch",
     "l20_pd_split_out",
     "l20_pd_fp8_e4m3_partial",
     "l20_pd_fp8_e4m3_merge",
@@ -141,6 +142,8 @@ def load(path: Optional[Path] = None) -> ctypes.CDLL:
     lib.l20_pd_set_spin_limit.restype = _i32
     lib.l20_pd_set_queue_counters.argtypes = [ctypes.c_uint64]
     lib.l20_pd_set_queue_counters.restype = _i32
+    lib.l20_pd_single_launch.argtypes = [ctypes.POINTER(L20PdFp8Args)]
+    lib.l20_pd_single_launch.restype = _i32
     lib.l20_pd_default_split_size.argtypes = [_i32, _i32, _i32, _i32]
     lib.l20_pd_default_split_size.restype = _i32
     lib.l20_pd_fp8_e4m3_dequant_f32.argtypes = [_vp, _vp, _i64, _f32, _vp]
@@ -298,6 +301,16 @@ def set_spin_limit(polls: int, lib: Optional[ctypes.CDLL] = None) -> None:
     lib = lib or load()
     if lib.l20_pd_set_spin_limit(int(polls)) != L20_PD_OK:
         raise RuntimeError(last_error(lib))
+
+
+def single_launch(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> bool:
+    """``l20_pd_single_launch``: whether ``split_out(args)`` runs as the single
+    launch on the current device (the workspace is then unused)."""
+    lib = lib or load()
+    rc = lib.l20_pd_single_launch(ctypes.byref(args))
+    if rc < 0:
+        raise RuntimeError(last_error(lib))
+    return rc == 1
 
 
 def set_queue_counters(value: int, lib: Optional[ctypes.CDLL] = None) -> None:

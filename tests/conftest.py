@@ -15,3 +15,16 @@ for p in (str(PKG), str(ROOT)):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X GPU (runs the HIP kernels)")
+
+
+import pytest  # noqa: E402
+
+
+@pytest.fixture(autouse=True)
+def _split_path_by_default(monkeypatch):
+    """By the library's own rule, small shapes run as one launch (one workgroup
+    per (sequence, KV head), no split workspace, no merge).  Tests of the split
+    kernels, the work queue and the merge pin the split path here; the tests of
+    the single launch ask for it (L20_PD_FUSED=1) or for the library's choice
+    (the variable removed)."""
+    monkeypatch.setenv("L20_PD_FUSED", "0")

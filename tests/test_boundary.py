@@ -189,6 +189,32 @@ def test_single_split_needs_no_workspace():
     cabi.check(a)
 
 
+def test_single_launch_rule(monkeypatch):
+    """l20_pd_single_launch reports the path split_out takes, on the host (no
+    GPU here: the CU count defaults to 256).  One launch for fp8 caches, one
+    query tile, at most one (sequence, KV head) pair per CU and at most 1024
+    tokens within reach; L20_PD_FUSED=0/1 overrides only the size rule."""
+    monkeypatch.delenv("L20_PD_FUSED", raising=False)
+    assert cabi.single_launch(valid_args())  # 8 x 4 pairs, 1024 tokens
+    longer = valid_args()
+    longer.max_seq_len, longer.partial_splits, longer.bt_max_pages = 1040, 5, 80  # 1280 tokens within reach
+    assert not cabi.single_launch(longer)
+    many = valid_args()
+    many.batch = 65  # 260 pairs
+    assert not cabi.single_launch(many)
+    drafts = valid_args()
+    drafts.q_len = 4  # 7 x 4 = 28 query columns: two tiles
+    assert not cabi.single_launch(drafts)
+    monkeypatch.setenv("L20_PD_FUSED", "1")
+    assert cabi.single_launch(longer) and cabi.single_launch(many) and not cabi.single_launch(drafts)
+    monkeypatch.setenv("L20_PD_FUSED", "0")
+    assert not cabi.single_launch(valid_args())
+    bad = valid_args()
+    bad.head_dim = 96
+    with pytest.raises(RuntimeError):
+        cabi.single_launch(bad)
+
+
 def test_empty_batch_is_a_noop():
     a = valid_args()
     a.batch = 0
