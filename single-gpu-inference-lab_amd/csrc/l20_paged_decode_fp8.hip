@@ -1727,7 +1727,8 @@ __device__ __forceinline__ void unpack_partial8(i32x4 r0, i32x4 r1, f32x4 &a, f3
 // ---------------------------------------------------------------------------
 // One workgroup of kFusedWaves waves per (sequence, KV head) pair: wave w
 // streams the w-th of kFusedWaves equal token ranges of the sequence (a
-// multiple of 32 tokens, at most 1024: one page-id register) through the
+// multiple of 32 tokens, at most 1024: one page-id register; blocks of 32
+// fp8 tokens or 16 tokens of a 16-bit cache) through the
 // partial kernel's per-unit math, NBF blocks in flight, and the waves'
 // online-softmax states meet in LDS, where every thread of the workgroup folds
 // them and writes output rows and LSE.  Nothing goes through the split
@@ -1756,8 +1757,8 @@ struct FoldSlots {
 
 template <typename QT, int KT, int D, int NBF>
 __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p) {
-  static_assert(KT != 1, "fp8 caches: 32-token blocks of two pages");
-  typedef KvUnit<QT, KT, D, 1, false, D == 128> U;
+  typedef KvUnit<QT, KT, D, 1, false, KT != 1 && D == 128> U;
+  constexpr int kTok = U::kTok;
   typedef typename U::Block Block;
   typedef typename U::qvec8 qvec8;
   __shared__ __attribute__((aligned(16))) char s_kx[U::kKLines ? kFusedWaves * U::kKxBytes : 16];
@@ -1778,7 +1779,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   const int start = wave * S;
   const int uEnd = min(start + S, L);
   const int tiles = max(0, (uEnd - start + kPage - 1) / kPage);
-  const int nU = (tiles + 1) >> 1;
+  const int nU = KT != 1 ? (tiles + 1) >> 1 : tiles;
 
   // page ids of the wave's range: lane t -> tile t (-1 past the range, past
   // the page list, and for an id outside the cache)
@@ -1821,7 +1822,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   auto step = [&](Block &r, int k) {
     int pg[2] = {-1, -1};
     if (k + NBF < nU) U::block_pages(pid, k + NBF, pg);
-    st.compute_block(r, pid, k, start + 32 * k, uEnd, draft0, lim, min_lim, tree, qop, c_log2, j, kx,
+    st.compute_block(r, pid, k, start + kTok * k, uEnd, draft0, lim, min_lim, tree, qop, c_log2, j, kx,
                      [&]() { U::load_pages(p, r, pg, kvh, 1, n16, j); });
     U::load_pages(p, r, pg, kvh, 2, n16, j);
   };
@@ -2465,9 +2466,13 @@ hipError_t launch_fused(const l20pd::PartialParams &pp, int head_dim, int batch,
   return hipGetLastError();
 }
 
-// Whether a call runs as the single launch: fp8 caches, one query tile (G x
-// q_len <= 16), no tree mask, at most one (sequence, KV head) pair per CU and
-// at most 1024 tokens per sequence the call may touch (four blocks per wave).
+// Whether a call runs as the single launch: one query tile (G x q_len <=
+// 16), no tree mask, at most one (sequence, KV head) pair per CU and at most
+// 1024 tokens per sequence the call may touch for fp8 caches (four blocks of
+// 32 tokens per wave), 640 for 16-bit ones (five blocks of 16 tokens, 8 KB
+// each as for fp8; 16-bit caches, 8 KV heads, per call: 4 x 512 tokens 16.1
+// -> 12.8 us, 32 x 512 19.2 -> 15.6, 4 x 640 16.3 -> 14.8, 1 x 2048 16.6
+// against 36.1).
 // Then every pair streams at once on its own CU and the split workspace and
 // the merge launch are skipped.  Measured in one process against the split
 // kernels (per call): config 1 10.0 -> 5.8 us, 64 x 1024 tokens (2 KV heads)
@@ -2478,13 +2483,13 @@ hipError_t launch_fused(const l20pd::PartialParams &pp, int head_dim, int batch,
 // L20_PD_FUSED=0/1 overrides the size rule (tests and measurement; the shape
 // conditions and kFusedMaxTokens always hold).
 bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
-  if (kv16 || nqt != 1 || a.tree_mask) return false;
+  if (nqt != 1 || a.tree_mask) return false;
   if (pp.l_cap > l20pd::kFusedMaxTokens) return false;
   if (const char *env = getenv("L20_PD_FUSED")) return env[0] == '1';
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  return (int64_t)a.batch * a.num_kv_heads <= cus && pp.l_cap <= 1024;
+  return (int64_t)a.batch * a.num_kv_heads <= cus && pp.l_cap <= (kv16 ? 640 : 1024);
 }
 
 template <typename QT, int D, int WPP>
@@ -2756,10 +2761,13 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   const int rows = a->batch * a->q_len;
   hipError_t e = hipSuccess;
   if (stages == kBoth && fused_fits(*a, pp, nqt, kv16)) {
-    e = e5m2 ? (bf16 ? launch_fused<__bf16, 2>(pp, a->head_dim, a->batch, a->num_kv_heads, stream)
-                     : launch_fused<_Float16, 2>(pp, a->head_dim, a->batch, a->num_kv_heads, stream))
-             : (bf16 ? launch_fused<__bf16, 0>(pp, a->head_dim, a->batch, a->num_kv_heads, stream)
-                     : launch_fused<_Float16, 0>(pp, a->head_dim, a->batch, a->num_kv_heads, stream));
+    const int D = a->head_dim, B = a->batch, H = a->num_kv_heads;
+    if (kv16)
+      e = bf16 ? launch_fused<__bf16, 1>(pp, D, B, H, stream) : launch_fused<_Float16, 1>(pp, D, B, H, stream);
+    else if (e5m2)
+      e = bf16 ? launch_fused<__bf16, 2>(pp, D, B, H, stream) : launch_fused<_Float16, 2>(pp, D, B, H, stream);
+    else
+      e = bf16 ? launch_fused<__bf16, 0>(pp, D, B, H, stream) : launch_fused<_Float16, 0>(pp, D, B, H, stream);
     if (e != hipSuccess) {
       snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
       return L20_PD_ELAUNCH;

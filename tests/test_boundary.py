@@ -205,6 +205,15 @@ def test_single_launch_rule(monkeypatch):
     drafts = valid_args()
     drafts.q_len = 4  # 7 x 4 = 28 query columns: two tiles
     assert not cabi.single_launch(drafts)
+    half = valid_args()  # 16-bit caches: up to 640 tokens within reach
+    half.kv_dtype, half.query_dtype = cabi.L20_PD_KV_FP16, cabi.L20_PD_FP16
+    half.max_seq_len, half.split_size, half.partial_splits = 640, 128, 6
+    half.po_stride_row, half.po_stride_head = 28 * 6 * 128, 6 * 128
+    half.pm_stride_row = half.ps_stride_row = 28 * 6
+    half.pm_stride_head = half.ps_stride_head = 6
+    assert cabi.single_launch(half)
+    half.max_seq_len = 656
+    assert not cabi.single_launch(half)
     monkeypatch.setenv("L20_PD_FUSED", "1")
     assert cabi.single_launch(longer) and cabi.single_launch(many) and not cabi.single_launch(drafts)
     monkeypatch.setenv("L20_PD_FUSED", "0")

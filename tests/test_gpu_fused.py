@@ -2,9 +2,10 @@
 each wave one eighth of the sequence, the waves' online-softmax states folded
 in LDS; no split workspace is written and no merge kernel runs.
 
-* Forced with L20_PD_FUSED=1 on every shape the path accepts (fp8 e4m3/e5m2,
-  head_dim 64/128, one query tile incl. draft rows, ragged and empty rows,
-  pages of 16/32/64 tokens, per-head scales, sequences up to 8192 tokens):
+* Forced with L20_PD_FUSED=1 on every shape the path accepts (fp8 e4m3/e5m2
+  and fp16/bf16 caches, block tables and CSR page lists, head_dim 64/128, one
+  query tile incl. draft rows, ragged and empty rows, pages of 16/32/64
+  tokens, per-head scales, sequences up to 8192 tokens):
   output and LSE against the oracle, through the torch op and the C ABI, and
   the workspace untouched (so the path that ran is the single launch).
 * The library's own choice (the variable unset): the single launch at
@@ -74,6 +75,45 @@ def test_single_launch_matches_oracle(case, monkeypatch):
         out, lse, untouched = _run_cabi(inp, split, pdt)
         assert untouched, "the split workspace was written: the single launch did not run"
         H.compare(out, lse, *exp)
+
+
+CASES16 = [
+    # name, batch, hq, hkv, d, lens, q_len, dtype, page, csr
+    ("fp16_ragged", 5, 28, 4, 128, [1, 15, 16, 33, 500], 1, torch.float16, 16, False),
+    ("bf16_d64_q2", 3, 16, 2, 64, [2, 300, 0], 2, torch.bfloat16, 16, False),
+    ("bf16_long_4096", 2, 16, 2, 128, [4096, 1000], 1, torch.bfloat16, 16, False),
+    ("fp16_pages_32", 4, 16, 2, 128, [1, 100, 511, 64], 1, torch.float16, 32, False),
+    ("bf16_csr", 4, 32, 8, 128, [1, 17, 480, 200], 1, torch.bfloat16, 16, True),
+]
+
+
+@pytest.mark.parametrize("case", CASES16, ids=[c[0] for c in CASES16])
+def test_single_launch_16bit_caches(case, monkeypatch):
+    """The same kernel over fp16/bf16 caches (16-token blocks): block tables
+    and CSR page lists, against the oracle, the workspace untouched."""
+    import l20_pd_cabi as cabi
+
+    name, batch, hq, hkv, d, lens, q_len, dtype, page, csr = case
+    monkeypatch.setenv("L20_PD_FUSED", "1")
+    inp = H.make_synthetic16(batch, hq, hkv, d, lens, q_len=q_len, dtype=dtype, page=page, csr_pad=2,
+                             seed=zlib.crc32(name.encode()) % 1000, garbage_tail=True)
+    exp = H.run_oracle16(inp, csr=csr)
+    po, pm, ps = H.workspace(inp, 256)
+    for t in (po, pm, ps):
+        t.fill_(float("nan"))
+    q = inp["query"]
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device)
+    table = inp["page_indices"] if csr else inp["block_table"]
+    args = cabi.args_from_tensors(q, inp["key_cache"], inp["value_cache"], table, inp["seq_lens"], po, pm, ps, out,
+                                  1.0, 1.0, inp["max_seq_len"], 256, softmax_scale=inp["softmax_scale"],
+                                  q_len=q_len, lse=lse, page_indptr=inp["page_indptr"] if csr else None)
+    assert cabi.single_launch(args)
+    cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(pm).all() and torch.isnan(po.float()).all()), "the split workspace was written"
+    H.compare(out, lse, *exp)
+    H.compare(*H.run_op16(inp, 64, csr=csr), *exp)
 
 
 @pytest.mark.parametrize("name,single", [("c1_qwen2.5_0.5b", True), ("c2_qwen2.5_coder_3b", False)])
