@@ -211,7 +211,7 @@ int32_t l20_pd_set_spin_limit(uint32_t polls);
  * -(error code) when the arguments fail l20_pd_fp8_e4m3_check.  Host only.  No
  * reference counterpart: the reference always runs its partial and reduce
  * kernels (l20_paged_decode.cu:692-723).  The single launch is taken for
- * G x q_len <= 16, no tree mask, batch x num_kv_heads <= the CU count and at
+ * G x q_len <= 32 (tree masks included), batch x num_kv_heads <= the CU count and at
  * most 1024 (fp8 caches) or 640 (16-bit caches) tokens per sequence within
  * reach of the call. */
 int32_t l20_pd_single_launch(const l20_pd_fp8_args *args);

@@ -1755,15 +1755,21 @@ struct FoldSlots {
   int64_t lse_srow, lse_shead;
 };
 
-template <typename QT, int KT, int D, int NBF>
+// NQT query tiles of 16 columns (G x q_len <= 16 NQT); TREE: ancestor-mask
+// verification as in the partial kernel.  The fold slots hold fp32 rows for
+// one tile and fp16 rows for two (fp32 would take 128 KB of LDS), the
+// precision of the 16-bit split workspaces.
+template <typename QT, int KT, int D, int NQT, bool TREE, int NBF>
 __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p) {
-  typedef KvUnit<QT, KT, D, 1, false, KT != 1 && D == 128> U;
+  typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128 && (NBF == 1 || NQT == 1)> U;
   constexpr int kTok = U::kTok;
+  constexpr int kCols = 16 * NQT;
+  typedef typename std::conditional<NQT == 1, float, _Float16>::type FT;
   typedef typename U::Block Block;
   typedef typename U::qvec8 qvec8;
   __shared__ __attribute__((aligned(16))) char s_kx[U::kKLines ? kFusedWaves * U::kKxBytes : 16];
-  __shared__ __attribute__((aligned(16))) float s_o[kFusedWaves][16][D];
-  __shared__ float s_m[kFusedWaves][16], s_l[kFusedWaves][16];
+  __shared__ __attribute__((aligned(16))) FT s_o[kFusedWaves][kCols][D];
+  __shared__ float s_m[kFusedWaves][kCols], s_l[kFusedWaves][kCols];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1799,15 +1805,23 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
       pid = (e >= 0 && v < p.num_pages) ? (int)v : -1;
     }
   }
-  qvec8 qop[1][U::NS];
+  qvec8 qop[NQT][U::NS];
   U::load_q(p, b, kvh, qop, n16, j);
+  int tree[TREE ? NQT : 1] = {};
+  U::load_tree(p, b, tree, n16);
   const float k_scale = p.k_scale_ph ? uniform_ld(p.k_scale_ph, kvh) : p.k_scale;
   const float v_scale = p.v_scale_ph ? uniform_ld(p.v_scale_ph, kvh) : p.v_scale;
   const float c_log2 = k_scale * p.qk_scale_log2;
+  // masking as in the partial kernel: keys before draft0 are seen by every
+  // column; draft key draft0 + j by draft row i when j <= i (causal: lim is
+  // the column's last visible key) or when bit j of its ancestor word is set
   const int draft0 = L - q_len;
-  const int lim[1] = {min(uEnd - 1, draft0 + n16 % q_len)};
-  const int min_lim = min(uEnd - 1, draft0);
-  const int tree[1] = {0};
+  int lim[TREE ? 1 : NQT] = {};
+  if constexpr (!TREE) {
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) lim[qt] = min(uEnd - 1, draft0 + (16 * qt + n16) % q_len);
+  }
+  const int min_lim = min(uEnd - 1, TREE ? draft0 - 1 : draft0);
 
   U st;
   st.reset();
@@ -1835,24 +1849,24 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   for (int i = 0; i < NBF - 1; ++i)
     if (k + i < nU) step(buf[i], k + i);
 
-  // every wave's (o / l, m, l) into its LDS slot: column 16 * 0 + n16 =
+  // every wave's (o / l, m, l) into its LDS slot: column 16 qt + n16 =
   // g * q_len + i at [wave][column]
   FoldSlots fs;
   fs.q_len = q_len;
   fs.group = p.group;
-  fs.po_kind = 0;
-  fs.po = &s_o[0][0][0];
+  fs.po_kind = NQT == 1 ? 0 : 1;
+  fs.po = reinterpret_cast<float *>(&s_o[0][0][0]);
   fs.po_srow = D;
   fs.po_shead = (int64_t)q_len * D;
-  fs.po_ssplit = 16 * D;
+  fs.po_ssplit = kCols * D;
   fs.pm = &s_m[0][0];
   fs.pm_srow = 1;
   fs.pm_shead = q_len;
-  fs.pm_ssplit = 16;
+  fs.pm_ssplit = kCols;
   fs.pl = &s_l[0][0];
   fs.pl_srow = 1;
   fs.pl_shead = q_len;
-  fs.pl_ssplit = 16;
+  fs.pl_ssplit = kCols;
   fs.out = nullptr;
   fs.o_srow = fs.o_shead = 0;
   fs.lse = nullptr;
@@ -1879,7 +1893,15 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
         if (l > 0.0f) {
           const float e = __builtin_amdgcn_exp2f(s_m[w][col] - mx) * l;
           wsum += e;
-          acc += e * *reinterpret_cast<const f32x4 *>(&s_o[w][col][d0]);
+          f32x4 o;
+          if constexpr (NQT == 1) {
+            o = *reinterpret_cast<const f32x4 *>(&s_o[w][col][d0]);
+          } else {
+            const f16x2 lo = *reinterpret_cast<const f16x2 *>(&s_o[w][col][d0]);
+            const f16x2 hi = *reinterpret_cast<const f16x2 *>(&s_o[w][col][d0 + 2]);
+            o = f32x4{(float)lo[0], (float)lo[1], (float)hi[0], (float)hi[1]};
+          }
+          acc += e * o;
         }
       }
     }
@@ -2457,22 +2479,40 @@ hipError_t launch_partial_shape(const l20pd::PartialParams &pp, int head_dim, in
 // shape measured: config 1 5.81 / 5.83 / 6.05 us, 128 x 1024 tokens 15.2 /
 // 17.8 / 26.3 us for two / three / four.)
 constexpr int kFusedNB = 2;
-template <typename QT, int KT>
-hipError_t launch_fused(const l20pd::PartialParams &pp, int head_dim, int batch, int num_kv_heads,
-                        hipStream_t stream) {
+// Two query tiles (verification: G x q_len up to 32) keep one block in
+// flight: two blocks (228 VGPRs, non-line K) measured slower on every
+// verify shape (64 Q / 8 KV heads, q_len 4: 4 x 1024 tokens 16.0 against
+// 18.9 us, 16 x 512 13.0 against 14.6).
+constexpr int kFusedNB2 = 1;
+template <typename QT, int KT, int NQT, bool TREE>
+hipError_t launch_fused_tiles(const l20pd::PartialParams &pp, int head_dim, int batch, int num_kv_heads,
+                              hipStream_t stream) {
   const dim3 grid((unsigned)((int64_t)batch * num_kv_heads)), block(64 * l20pd::kFusedWaves);
-  if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, kFusedNB>), grid, block, 0, stream, pp);
-  else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, kFusedNB>), grid, block, 0, stream, pp);
+  constexpr int NB = NQT == 1 ? kFusedNB : kFusedNB2;
+  if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, NQT, TREE, NB>), grid, block, 0, stream, pp);
+  else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, NQT, TREE, NB>), grid, block, 0, stream, pp);
   return hipGetLastError();
 }
+template <typename QT, int KT>
+hipError_t launch_fused(const l20pd::PartialParams &pp, int head_dim, int nqt, int batch, int num_kv_heads,
+                        hipStream_t stream) {
+  if (nqt == 1)
+    return pp.tree ? launch_fused_tiles<QT, KT, 1, true>(pp, head_dim, batch, num_kv_heads, stream)
+                   : launch_fused_tiles<QT, KT, 1, false>(pp, head_dim, batch, num_kv_heads, stream);
+  return pp.tree ? launch_fused_tiles<QT, KT, 2, true>(pp, head_dim, batch, num_kv_heads, stream)
+                 : launch_fused_tiles<QT, KT, 2, false>(pp, head_dim, batch, num_kv_heads, stream);
+}
 
-// Whether a call runs as the single launch: one query tile (G x q_len <=
-// 16), no tree mask, at most one (sequence, KV head) pair per CU and at most
+// Whether a call runs as the single launch (one or two query tiles, causal
+// draft rows or a tree mask): at most one (sequence, KV head) pair per CU and
+// at most
 // 1024 tokens per sequence the call may touch for fp8 caches (four blocks of
 // 32 tokens per wave), 640 for 16-bit ones (five blocks of 16 tokens, 8 KB
 // each as for fp8; 16-bit caches, 8 KV heads, per call: 4 x 512 tokens 16.1
 // -> 12.8 us, 32 x 512 19.2 -> 15.6, 4 x 640 16.3 -> 14.8, 1 x 2048 16.6
-// against 36.1).
+// against 36.1).  Verification (64 Q / 8 KV heads, q_len 4, per call): 16 x
+// 512 tokens 20.7 -> 13.0 us, 4 x 1024 19.0 -> 16.0, 8 x 1024 with 32 Q / 4
+// KV heads 15.7 either way.
 // Then every pair streams at once on its own CU and the split workspace and
 // the merge launch are skipped.  Measured in one process against the split
 // kernels (per call): config 1 10.0 -> 5.8 us, 64 x 1024 tokens (2 KV heads)
@@ -2483,7 +2523,7 @@ hipError_t launch_fused(const l20pd::PartialParams &pp, int head_dim, int batch,
 // L20_PD_FUSED=0/1 overrides the size rule (tests and measurement; the shape
 // conditions and kFusedMaxTokens always hold).
 bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
-  if (nqt != 1 || a.tree_mask) return false;
+  if (nqt > 2) return false;  // (the checks already limit G x q_len to 32)
   if (pp.l_cap > l20pd::kFusedMaxTokens) return false;
   if (const char *env = getenv("L20_PD_FUSED")) return env[0] == '1';
   int dev = 0, cus = 256;
@@ -2763,11 +2803,11 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
   if (stages == kBoth && fused_fits(*a, pp, nqt, kv16)) {
     const int D = a->head_dim, B = a->batch, H = a->num_kv_heads;
     if (kv16)
-      e = bf16 ? launch_fused<__bf16, 1>(pp, D, B, H, stream) : launch_fused<_Float16, 1>(pp, D, B, H, stream);
+      e = bf16 ? launch_fused<__bf16, 1>(pp, D, nqt, B, H, stream) : launch_fused<_Float16, 1>(pp, D, nqt, B, H, stream);
     else if (e5m2)
-      e = bf16 ? launch_fused<__bf16, 2>(pp, D, B, H, stream) : launch_fused<_Float16, 2>(pp, D, B, H, stream);
+      e = bf16 ? launch_fused<__bf16, 2>(pp, D, nqt, B, H, stream) : launch_fused<_Float16, 2>(pp, D, nqt, B, H, stream);
     else
-      e = bf16 ? launch_fused<__bf16, 0>(pp, D, B, H, stream) : launch_fused<_Float16, 0>(pp, D, B, H, stream);
+      e = bf16 ? launch_fused<__bf16, 0>(pp, D, nqt, B, H, stream) : launch_fused<_Float16, 0>(pp, D, nqt, B, H, stream);
     if (e != hipSuccess) {
       snprintf(g_last_error, sizeof(g_last_error), "HIP launch failed: %s", hipGetErrorString(e));
       return L20_PD_ELAUNCH;

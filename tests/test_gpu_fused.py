@@ -11,8 +11,10 @@ in LDS; no split workspace is written and no merge kernel runs.
 * The library's own choice (the variable unset): the single launch at
   config 1 and for short sequences, the split kernels at config 2 (2048
   tokens per sequence), both against the oracle.
-* Shapes outside the path (two query tiles, more tokens than it covers) run
-  the split kernels even when it is asked for.
+* Verification: draft rows (causal) and random ancestor trees over one and
+  two query tiles, forced and by the library's choice.
+* Sequences longer than the path covers run the split kernels even when it
+  is asked for.
 """
 
 import zlib
@@ -40,7 +42,7 @@ CASES = [
 ]
 
 
-def _run_cabi(inp, split, pdt):
+def _run_cabi(inp, split, pdt=torch.float32):
     """The C ABI with a NaN-filled workspace; returns (out, lse, workspace
     untouched)."""
     import l20_pd_cabi as cabi
@@ -56,7 +58,7 @@ def _run_cabi(inp, split, pdt):
     args = cabi.args_from_tensors(q, inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
                                   po, pm, ps, out, ks, vs, inp["max_seq_len"], split,
                                   softmax_scale=inp["softmax_scale"], q_len=inp["q_len"], lse=lse,
-                                  k_scale_per_head=ksph, v_scale_per_head=vsph)
+                                  k_scale_per_head=ksph, v_scale_per_head=vsph, tree_mask=inp.get("tree_mask"))
     cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     untouched = bool(torch.isnan(pm).all() and torch.isnan(ps).all() and torch.isnan(po.float()).all())
@@ -140,14 +142,51 @@ def test_library_takes_the_single_launch_for_short_sequences(monkeypatch):
     H.compare(out, lse, *H.run_oracle(inp))
 
 
-@pytest.mark.parametrize("case", [
-    ("two_query_tiles", 2, 32, 2, 128, [300, 40], 2),     # G x q_len = 32
-    ("beyond_8192", 1, 16, 2, 128, [9000], 1),
-])
-def test_shapes_outside_the_single_launch_use_the_split_kernels(case, monkeypatch):
-    name, batch, hq, hkv, d, lens, q_len = case
+TILES = [
+    # name, batch, hq, hkv, d, lens, q_len, tree
+    ("verify_2tiles", 4, 64, 8, 128, [1024, 17, 300, 4], 4, False),
+    ("verify_2tiles_d64", 3, 32, 4, 64, [700, 64, 1], 4, False),
+    ("tree_1tile", 3, 8, 2, 128, [700, 37, 1500], 4, True),
+    ("tree_2tiles", 2, 16, 2, 128, [1000, 333], 4, True),
+    ("tree_mha_d64", 2, 32, 32, 64, [530, 64], 8, True),
+    ("tree_32drafts", 2, 4, 4, 128, [900, 32], 32, True),
+]
+
+
+@pytest.mark.parametrize("case", TILES, ids=[c[0] for c in TILES])
+def test_single_launch_draft_rows_and_trees(case, monkeypatch):
+    """Verification: draft rows under the causal rule or a random ancestor tree,
+    one or two 16-column query tiles (fp16 fold slots for two), against the
+    oracle; the workspace untouched."""
+    import numpy as np
+    from test_gpu_tree_verify import random_tree, words
+
+    name, batch, hq, hkv, d, lens, q_len, tree = case
     monkeypatch.setenv("L20_PD_FUSED", "1")
-    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, seed=zlib.crc32(name.encode()) % 1000)
+    inp = H.make_synthetic(batch, hq, hkv, d, lens, q_len=q_len, seed=zlib.crc32(name.encode()) % 1000,
+                           garbage_tail=True)
+    if tree:
+        rng = np.random.default_rng(zlib.crc32(name.encode()))
+        inp["tree_mask"] = words(np.stack([random_tree(q_len, rng) for _ in range(batch)])).cuda()
+    exp = H.run_oracle(inp)
+    for split in (64, 1024):
+        out, lse, untouched = _run_cabi(inp, split)
+        assert untouched, "the split workspace was written: the single launch did not run"
+        H.compare(out, lse, *exp)
+    H.compare(*H.run_op(inp, 256, via="torch"), *exp)
+
+
+def test_library_takes_the_single_launch_for_small_verify_batches(monkeypatch):
+    monkeypatch.delenv("L20_PD_FUSED", raising=False)
+    inp = H.make_synthetic(16, 64, 8, 128, [512 - 9 * i for i in range(16)], q_len=4, seed=9)
+    out, lse, untouched = _run_cabi(inp, 128)
+    assert untouched
+    H.compare(out, lse, *H.run_oracle(inp))
+
+
+def test_sequences_beyond_the_single_launch_use_the_split_kernels(monkeypatch):
+    monkeypatch.setenv("L20_PD_FUSED", "1")
+    inp = H.make_synthetic(1, 16, 2, 128, [9000], seed=19)
     out, lse, untouched = _run_cabi(inp, 256, torch.float32)
     assert not untouched
     H.compare(out, lse, *H.run_oracle(inp))
