@@ -228,3 +228,29 @@ def test_single_launch_graph_replays_match_eager(monkeypatch):
         assert torch.equal(out, eager[0]) and torch.equal(lse, eager[1])
         cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
+
+
+def test_noalloc_entry_takes_the_single_launch(monkeypatch):
+    """The allocation-free entry point runs the same rule: a small batch takes
+    the single launch (its scratch array is not needed) and matches the oracle
+    and the allocating entry point bitwise."""
+    import l20_pd_cabi as cabi
+
+    monkeypatch.delenv("L20_PD_FUSED", raising=False)
+    inp = H.make_synthetic(5, 28, 4, 128, [1, 15, 16, 33, 1000], seed=31)
+    exp = H.run_oracle(inp)
+    q = inp["query"]
+    outs = []
+    for noalloc in (False, True):
+        po, pm, ps = H.workspace(inp, 256)
+        out = torch.empty_like(q)
+        lse = torch.empty(q.shape[0], q.shape[1], dtype=torch.float32, device=q.device)
+        args = cabi.args_from_tensors(q, inp["key_cache"], inp["value_cache"], inp["block_table"], inp["seq_lens"],
+                                      po, pm, ps, out, inp["k_scale"], inp["v_scale"], inp["max_seq_len"], 256,
+                                      softmax_scale=inp["softmax_scale"], lse=lse)
+        assert cabi.single_launch(args)
+        (cabi.split_out_noalloc if noalloc else cabi.split_out)(args, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        H.compare(out, lse, *exp)
+        outs.append((out, lse))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
