@@ -335,8 +335,11 @@ def run_decode(args, mode):
     h = stream.cuda_stream
     # Small batches of short sequences run as one launch (pd_fp8_fused, no
     # merge): that kernel is then the call, and the roofline times it as such.
-    single = cabi.single_launch(calls[0][0], lib)
-    kernel = "pd_fp8_fused" if single else "pd_fp8_partial"
+    # Batches whose 512-token splits fill the CUs once run the partial stage
+    # as that kernel's split mode (then the merge): the roofline times it.
+    path = cabi.launch_path(calls[0][0], lib)
+    single = path == 1
+    kernel = "pd_fp8_fused" if path else "pd_fp8_partial"
     kernel_fn = cabi.split_out if single else cabi.partial
 
     settle_calls, settle_ms = settle(lambda i: cabi.split_out(calls[i % n_sets][0], h, lib), args.settle_ms)

@@ -207,13 +207,17 @@ int32_t l20_pd_set_spin_limit(uint32_t polls);
 /* 1 if l20_pd_fp8_e4m3_split_out (or l20_pd_split_out) runs `args` on the
  * current device as the single launch -- one workgroup per (sequence, KV
  * head), the splits folded in LDS, the partial_* workspace neither read nor
- * written, no merge launch -- and 0 if as the partial and merge kernels;
- * -(error code) when the arguments fail l20_pd_fp8_e4m3_check.  Host only.  No
- * reference counterpart: the reference always runs its partial and reduce
- * kernels (l20_paged_decode.cu:692-723).  The single launch is taken for
- * G x q_len <= 32 (tree masks included), batch x num_kv_heads <= the CU count and at
- * most 1024 (fp8 caches) or 640 (16-bit caches) tokens per sequence within
- * reach of the call. */
+ * written, no merge launch --; 2 if its partial stage runs as that kernel's
+ * split mode (one workgroup per (split, sequence, KV head), each writing its
+ * split's partial) followed by the merge; 0 if as the persistent partial
+ * kernel and the merge; -(error code) when the arguments fail
+ * l20_pd_fp8_e4m3_check.  Host only.  No reference counterpart: the reference
+ * always runs its partial and reduce kernels (l20_paged_decode.cu:692-723).
+ * The single launch is taken for G x q_len <= 32 (tree masks included),
+ * batch x num_kv_heads <= the CU count and at most 1024 (fp8 caches) or 640
+ * (16-bit caches) tokens per sequence within reach of the call; the split
+ * mode for 512-token splits whose batch x num_kv_heads x splits triples fill
+ * more than half the CUs without exceeding them. */
 int32_t l20_pd_single_launch(const l20_pd_fp8_args *args);
 
 /* Sets every work-queue counter of the current device to `value` (after a

@@ -135,6 +135,10 @@ struct PartialParams {
   // ceil(2^32 / page_mult) (page_mult > 1): T / page_mult = umulhi(T, magic),
   // exact for T < 2^32 / page_mult (the host bounds max_seq_len for it).
   unsigned int page_magic;
+  // pd_fp8_fused only: 0 = one workgroup per (sequence, KV head) covers the
+  // whole sequence; otherwise the split size, one workgroup per (split,
+  // sequence, KV head) writing the split's partial for the merge.
+  int fused_split;
 };
 
 // ---------------------------------------------------------------------------
@@ -1735,6 +1739,15 @@ __device__ __forceinline__ void unpack_partial8(i32x4 r0, i32x4 r1, f32x4 &a, f3
 // workspace and no merge kernel runs: for a batch whose pairs fit the CUs at
 // once this is the whole call (the host's fused_fits decides; l20_pd_single_launch
 // reports it).
+// Split mode (p.fused_split = the split size S): one workgroup per (split,
+// sequence, KV head), wave w streaming tokens [sS + wS/8, sS + (w+1)S/8) of
+// split s, the waves folded in LDS as above; a sequence of one split writes
+// its output rows and LSE (and marks slot 0 final), the others write split
+// s's partial (o / l, m, l) into the workspace, and the merge kernel
+// finishes them.  For batches whose (split, sequence, KV head) triples fit
+// the CUs at once with a few blocks per wave: the whole KV streams in one
+// burst, where the persistent partial kernel keeps two blocks per wave in
+// flight over longer units.
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxTokens = kFusedWaves * 1024;
 
@@ -1775,36 +1788,45 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15;
   const int j = lane >> 4;
-  const int b = (int)(blockIdx.x / (unsigned)p.num_kv_heads);
-  const int kvh = (int)blockIdx.x - b * p.num_kv_heads;
+  const int SS = p.fused_split;
+  const unsigned int pairs = (unsigned int)p.batch * (unsigned int)p.num_kv_heads;
+  const int split = SS ? (int)(blockIdx.x / pairs) : 0;
+  const int pair = (int)(blockIdx.x - (unsigned int)split * pairs);
+  const int b = pair / p.num_kv_heads;
+  const int kvh = pair - b * p.num_kv_heads;
   char *const kx = s_kx + (U::kKLines ? wave * U::kKxBytes : 0);
   const int q_len = p.q_len;
-  // (the host launches this kernel only when l_cap <= kFusedMaxTokens)
-  const int L = min(clamped_len(p, b), kFusedMaxTokens);
-  const int S = max(32, ((L + kFusedWaves - 1) / kFusedWaves + 31) & ~31);
-  const int start = wave * S;
-  const int uEnd = min(start + S, L);
-  const int tiles = max(0, (uEnd - start + kPage - 1) / kPage);
-  const int nU = KT != 1 ? (tiles + 1) >> 1 : tiles;
-
+  // (whole sequences: the host launches this kernel only when l_cap <=
+  // kFusedMaxTokens; splits: the host checks S / kFusedWaves <= 1024 and
+  // the block size divides it)
   // page ids of the wave's range: lane t -> tile t (-1 past the range, past
   // the page list, and for an id outside the cache)
   const int32_t *row = p.indptr ? p.bt + uniform_ld(p.indptr, b) : p.bt + (int64_t)b * p.bt_srow;
   const int npages = p.indptr ? uniform_ld(p.indptr, b + 1) - uniform_ld(p.indptr, b) : p.bt_pages;
-  int pid = -1;
-  if (lane < tiles && lane < npages * p.page_mult - start / kPage) {
-    const int T = start / kPage + lane;
+  auto tile_id = [&](int T) {
     const int m = p.page_mult;
     if (m == 1) {
       const int e = row[T];
-      pid = (e >= 0 && (int64_t)e < p.num_pages) ? e : -1;
-    } else {
-      const int qq = (int)__umulhi((unsigned int)T, p.page_magic);  // T / m
-      const int e = row[qq];
-      const int64_t v = (int64_t)e * m + (T - qq * m);
-      pid = (e >= 0 && v < p.num_pages) ? (int)v : -1;
+      return (e >= 0 && (int64_t)e < p.num_pages) ? e : -1;
     }
-  }
+    const int qq = (int)__umulhi((unsigned int)T, p.page_magic);  // T / m
+    const int e = row[qq];
+    const int64_t v = (int64_t)e * m + (T - qq * m);
+    return (e >= 0 && v < p.num_pages) ? (int)v : -1;
+  };
+  const int L = SS ? clamped_len(p, b) : min(clamped_len(p, b), kFusedMaxTokens);
+  const int n_b = SS ? splits_of_len(L, SS) : 1;
+  if (split >= n_b) return;  // the sequence has no such split (the whole workgroup)
+  const int sEnd = SS ? min((split + 1) * SS, L) : L;
+  // (split mode: loading the span's page ids with the length instead, before
+  // it is known, measured 0.15-0.2 us slower per call)
+  const int S = SS ? SS / kFusedWaves : max(32, ((L + kFusedWaves - 1) / kFusedWaves + 31) & ~31);
+  const int start = split * SS + wave * S;
+  const int uEnd = min(start + S, sEnd);
+  const int tiles = max(0, (uEnd - start + kPage - 1) / kPage);
+  const int nU = KT != 1 ? (tiles + 1) >> 1 : tiles;
+  int pid = -1;
+  if (lane < tiles && lane < npages * p.page_mult - start / kPage) pid = tile_id(start / kPage + lane);
   qvec8 qop[NQT][U::NS];
   U::load_q(p, b, kvh, qop, n16, j);
   int tree[TREE ? NQT : 1] = {};
@@ -1910,6 +1932,25 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
     const int i = col - g * q_len;
     const int64_t orow = (int64_t)b * q_len + i;
     const int64_t h = (int64_t)kvh * p.group + g;
+    if (n_b > 1) {
+      // split mode: this split's partial, in the workspace's element type
+      const int64_t po_idx = orow * p.po_srow + h * p.po_shead + split * p.po_ssplit + d0;
+      if (p.po_kind == 0) {
+        *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.po) + po_idx) = acc * inv;
+      } else {
+        _Float16 *dst = reinterpret_cast<_Float16 *>(p.po) + po_idx;
+        *reinterpret_cast<i32x2 *>(dst) =
+            p.po_kind == 2 ? i32x2{pack2<__bf16>(acc[0] * inv, acc[1] * inv), pack2<__bf16>(acc[2] * inv, acc[3] * inv)}
+                           : i32x2{pack2<_Float16>(acc[0] * inv, acc[1] * inv), pack2<_Float16>(acc[2] * inv, acc[3] * inv)};
+      }
+      if (d0 == 0) {
+        p.pm[orow * p.pm_srow + h * p.pm_shead + split * p.pm_ssplit] = mx;
+        p.pl[orow * p.pl_srow + h * p.pl_shead + split * p.pl_ssplit] = wsum;
+      }
+      continue;
+    }
+    // merge: the row is final (a sequence of one split, split mode)
+    if (SS && d0 == 0 && p.num_splits > 1) p.pm[orow * p.pm_srow + h * p.pm_shead] = INFINITY;
     QT *dst = reinterpret_cast<QT *>(p.out) + orow * p.o_srow + h * p.o_shead + d0;
     *reinterpret_cast<i32x2 *>(dst) = i32x2{pack2<QT>(acc[0] * inv, acc[1] * inv), pack2<QT>(acc[2] * inv, acc[3] * inv)};
     if (d0 == 0 && p.lse)
@@ -2487,7 +2528,9 @@ constexpr int kFusedNB2 = 1;
 template <typename QT, int KT, int NQT, bool TREE>
 hipError_t launch_fused_tiles(const l20pd::PartialParams &pp, int head_dim, int batch, int num_kv_heads,
                               hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)batch * num_kv_heads)), block(64 * l20pd::kFusedWaves);
+  // split mode: one workgroup per (split, sequence, KV head), split-major
+  const dim3 grid((unsigned)((int64_t)batch * num_kv_heads * (pp.fused_split ? pp.num_splits : 1))),
+      block(64 * l20pd::kFusedWaves);
   constexpr int NB = NQT == 1 ? kFusedNB : kFusedNB2;
   if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, NQT, TREE, NB>), grid, block, 0, stream, pp);
   else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, NQT, TREE, NB>), grid, block, 0, stream, pp);
@@ -2530,6 +2573,35 @@ bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nq
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
   return (int64_t)a.batch * a.num_kv_heads <= cus && pp.l_cap <= (kv16 ? 640 : 1024);
+}
+
+// Whether the partial stage of a split call runs as the single-launch kernel's
+// split mode (one workgroup per (split, sequence, KV head), its waves' states
+// folded in LDS, the split's partial written for the merge) rather than the
+// persistent partial kernel: each wave's share of a split (S / 8 tokens) must
+// be whole blocks and fit one page-id register, and by the size rule the
+// split is 512 tokens (two fp8 blocks per wave, all in flight at once) and
+// the (split, sequence, KV head) triples fill more than half the CUs without
+// exceeding them: one 8-wave workgroup per CU, the whole KV in one burst.
+// Measured in one process against the persistent kernel at the library's
+// split, 33.5 MB of KV per call, µs per call: 32 x 2048 tokens, 2 KV heads
+// (config 2) 13.5-13.9 against 14.7; 16 x 2048, 4 KV heads 14.1 against
+// 17.6; 8 x 4096, 4 KV heads 13.9 against 17.7; 4 x 4096, 8 KV heads 14.2
+// against 17.4; 1 x 16384, 8 KV heads 14.7 against 18.2; verification
+// (4 x 4096, 64 / 8 heads, q_len 4) 19.9 against 24.5.  With twice the
+// triples (64 x 2048, 2 KV heads: two rounds) 23.8 against 19.5, and with
+// 256 or 1024-token splits at config 2 17.4 and 15.3.  L20_PD_FUSED_SPLIT=0/1
+// overrides the size rule.
+bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
+  if (nqt > 2 || pp.num_splits < 2) return false;
+  const int blk = kv16 ? 16 : 32;
+  if (a.split_size % (l20pd::kFusedWaves * blk) != 0 || a.split_size / l20pd::kFusedWaves > 1024) return false;
+  if (const char *env = getenv("L20_PD_FUSED_SPLIT")) return env[0] == '1';
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int64_t triples = (int64_t)a.batch * a.num_kv_heads * pp.num_splits;
+  return a.split_size == 512 && 2 * triples > cus && triples <= cus;
 }
 
 template <typename QT, int D, int WPP>
@@ -2814,7 +2886,17 @@ int32_t run(const l20_pd_fp8_args *a, void *stream_ptr, int stages, int kinds) {
     }
     return L20_PD_OK;
   }
-  if (stages & kPartial) {
+  if ((stages & kPartial) && fused_split_fits(*a, pp, nqt, kv16)) {
+    const int D = a->head_dim, B = a->batch, H = a->num_kv_heads;
+    l20pd::PartialParams ps = pp;
+    ps.fused_split = a->split_size;
+    if (kv16)
+      e = bf16 ? launch_fused<__bf16, 1>(ps, D, nqt, B, H, stream) : launch_fused<_Float16, 1>(ps, D, nqt, B, H, stream);
+    else if (e5m2)
+      e = bf16 ? launch_fused<__bf16, 2>(ps, D, nqt, B, H, stream) : launch_fused<_Float16, 2>(ps, D, nqt, B, H, stream);
+    else
+      e = bf16 ? launch_fused<__bf16, 0>(ps, D, nqt, B, H, stream) : launch_fused<_Float16, 0>(ps, D, nqt, B, H, stream);
+  } else if (stages & kPartial) {
     const int D = a->head_dim, B = a->batch, H = a->num_kv_heads;
     if (kv16)
       e = bf16 ? launch_partial_shape<__bf16, 1>(pp, D, nqt, B, H, stream)
@@ -2913,6 +2995,14 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
   // contexts (fewer partials to merge), and at least ~8 splits per sequence
   // for short contexts, where the launch is latency-bound.
   if (max_seq_len > 32768) return 1024;
+  // Beyond the single launch's reach (1024 tokens), a batch whose 512-token
+  // (split, sequence, KV head) triples fill more than half the CUs without
+  // exceeding them runs the single-launch kernel's split mode at 512.
+  {
+    const int64_t cus = cu_count > 0 ? cu_count : 256;
+    const int64_t triples = (int64_t)batch * (num_kv_heads > 0 ? num_kv_heads : 1) * l20_pd_num_splits(max_seq_len, 512);
+    if (max_seq_len > 1024 && 2 * triples > cus && triples <= cus) return 512;
+  }
   int32_t s = 512;
   while (s > 64 && (int64_t)s * 8 > max_seq_len) s >>= 1;
   // Double the split while that lets every (sequence, split) item of a batch
@@ -2958,7 +3048,7 @@ int32_t l20_pd_single_launch(const l20_pd_fp8_args *a) {
   const int n_s = l20_pd_num_splits(a->max_seq_len, a->split_size);
   const int nqt = (a->num_q_heads / a->num_kv_heads * a->q_len + 15) / 16;
   const l20pd::PartialParams pp = partial_params(*a, n_s);
-  return fused_fits(*a, pp, nqt, kv16) ? 1 : 0;
+  return fused_fits(*a, pp, nqt, kv16) ? 1 : fused_split_fits(*a, pp, nqt, kv16) ? 2 : 0;
 }
 
 int32_t l20_pd_set_queue_counters(uint64_t value) {

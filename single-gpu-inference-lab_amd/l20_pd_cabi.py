@@ -313,6 +313,17 @@ def single_launch(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> bool
     return rc == 1
 
 
+def launch_path(args: L20PdFp8Args, lib: Optional[ctypes.CDLL] = None) -> int:
+    """``l20_pd_single_launch``'s code: 1 the single launch (no workspace, no
+    merge), 2 the single-launch kernel's split mode for the partial stage
+    (then the merge), 0 the persistent partial kernel and the merge."""
+    lib = lib or load()
+    rc = lib.l20_pd_single_launch(ctypes.byref(args))
+    if rc < 0:
+        raise RuntimeError(last_error(lib))
+    return int(rc)
+
+
 def set_queue_counters(value: int, lib: Optional[ctypes.CDLL] = None) -> None:
     """``l20_pd_set_queue_counters``: every work-queue counter of the current
     device set to ``value`` (a test hook; ``device_errors(clear=True)`` zeroes

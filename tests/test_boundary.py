@@ -56,8 +56,14 @@ def test_num_splits_and_default_split_size():
     # items fill at most half the grid (32 x 8 items on 1024 slots -> 128)
     assert lib.l20_pd_default_split_size(2, 8, 131072, 256) == 1024
     assert lib.l20_pd_default_split_size(128, 4, 8192, 256) == 512
-    assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 128
     assert lib.l20_pd_default_split_size(64, 2, 2048, 256) == 256
+    # 512 when the 512-token (split, sequence, KV head) triples of a batch
+    # beyond 1024 tokens fill more than half the CUs without exceeding them
+    # (the single-launch kernel's split mode): 32 x 2 x 4 = 256 triples
+    assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 512
+    assert lib.l20_pd_default_split_size(1, 8, 16384, 256) == 512
+    assert lib.l20_pd_default_split_size(32, 2, 2048, 512) != 512  # 256 triples: half of 512 CUs
+    assert lib.l20_pd_default_split_size(32, 2, 2048, 128) != 512  # 256 triples on 128 CUs
     assert lib.l20_pd_default_split_size(4, 2, 512, 256) == 64
     # doubled when that fits every item in one round of the persistent grid
     # (64 sequences x 4 splits on 256 one-workgroup CUs), never past 1024
@@ -223,6 +229,51 @@ def test_single_launch_rule(monkeypatch):
     bad.head_dim = 96
     with pytest.raises(RuntimeError):
         cabi.single_launch(bad)
+
+
+def _with_split(a, split):
+    """``a`` with its workspace shaped for ``split``: one slot per split."""
+    n = -(-a.max_seq_len // split)
+    a.split_size, a.partial_splits = split, n
+    a.po_stride_row, a.po_stride_head, a.po_stride_split = 28 * n * 128, n * 128, 128
+    a.pm_stride_row = a.ps_stride_row = 28 * n
+    a.pm_stride_head = a.ps_stride_head = n
+    return a
+
+
+def test_split_mode_rule(monkeypatch):
+    """l20_pd_single_launch returns 2 when the partial stage runs as the
+    single-launch kernel's split mode (one workgroup per (split, sequence, KV
+    head), merge after): 512-token splits whose triples fill more than half
+    the CUs (256 here, no GPU) without exceeding them; L20_PD_FUSED_SPLIT=0/1
+    overrides the size rule, not the shape conditions."""
+    monkeypatch.delenv("L20_PD_FUSED", raising=False)
+    monkeypatch.delenv("L20_PD_FUSED_SPLIT", raising=False)
+    a = valid_args()  # 28 query / 4 KV heads
+    a.max_seq_len, a.bt_stride_row, a.bt_max_pages = 2048, 128, 128
+    a.batch = 16
+    _with_split(a, 512)
+    assert cabi.launch_path(a) == 2  # 16 x 4 x 4 = 256 triples
+    assert not cabi.single_launch(a)
+    a.batch = 8  # 128 triples: half the CUs
+    assert cabi.launch_path(a) == 0
+    a.batch = 17  # 272 triples
+    assert cabi.launch_path(a) == 0
+    a.batch = 16
+    _with_split(a, 256)  # other splits: the persistent kernel
+    assert cabi.launch_path(a) == 0
+    monkeypatch.setenv("L20_PD_FUSED_SPLIT", "1")
+    assert cabi.launch_path(a) == 2
+    _with_split(a, 384)  # 48 tokens per wave: not whole fp8 blocks
+    assert cabi.launch_path(a) == 0
+    monkeypatch.setenv("L20_PD_FUSED_SPLIT", "0")
+    _with_split(a, 512)
+    assert cabi.launch_path(a) == 0
+    a.max_seq_len, a.bt_max_pages = 1024, 64  # within the single launch's reach
+    monkeypatch.delenv("L20_PD_FUSED_SPLIT")
+    _with_split(a, 512)
+    a.batch = 32  # 128 pairs: the single launch first
+    assert cabi.launch_path(a) == 1
 
 
 def test_empty_batch_is_a_noop():
