@@ -26,5 +26,8 @@ def _split_path_by_default(monkeypatch):
     per (sequence, KV head), no split workspace, no merge).  Tests of the split
     kernels, the work queue and the merge pin the split path here; the tests of
     the single launch ask for it (L20_PD_FUSED=1) or for the library's choice
-    (the variable removed)."""
+    (the variable removed).  Likewise the single-launch kernel's split mode
+    (512-token splits whose triples fill the CUs once) is off unless a test
+    asks for it (L20_PD_FUSED_SPLIT=1) or for the library's choice."""
     monkeypatch.setenv("L20_PD_FUSED", "0")
+    monkeypatch.setenv("L20_PD_FUSED_SPLIT", "0")
