@@ -2596,11 +2596,13 @@ bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, 
   if (nqt > 2 || pp.num_splits < 2) return false;
   const int blk = kv16 ? 16 : 32;
   if (a.split_size % (l20pd::kFusedWaves * blk) != 0 || a.split_size / l20pd::kFusedWaves > 1024) return false;
+  // one workgroup per triple: the grid's x dimension bounds them (forced calls included)
+  const int64_t triples = (int64_t)a.batch * a.num_kv_heads * pp.num_splits;
+  if (triples >= ((int64_t)1 << 31)) return false;
   if (const char *env = getenv("L20_PD_FUSED_SPLIT")) return env[0] == '1';
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  const int64_t triples = (int64_t)a.batch * a.num_kv_heads * pp.num_splits;
   return a.split_size == 512 && 2 * triples > cus && triples <= cus;
 }
 
