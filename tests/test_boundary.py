@@ -56,12 +56,15 @@ def test_num_splits_and_default_split_size():
     # items fill at most half the grid (32 x 8 items on 1024 slots -> 128)
     assert lib.l20_pd_default_split_size(2, 8, 131072, 256) == 1024
     assert lib.l20_pd_default_split_size(128, 4, 8192, 256) == 512
-    assert lib.l20_pd_default_split_size(64, 2, 2048, 256) == 256
+    assert lib.l20_pd_default_split_size(64, 2, 2048, 256) == 1024  # 512 triples at 512, 256 at 1024
+    assert lib.l20_pd_default_split_size(64, 2, 2048, 512) == 512  # 512 triples on 512 CUs
+    assert lib.l20_pd_default_split_size(128, 2, 2048, 256) == 256  # 512 triples at 1024: the persistent rules
     # 512 when the 512-token (split, sequence, KV head) triples of a batch
     # beyond 1024 tokens fill more than half the CUs without exceeding them
     # (the single-launch kernel's split mode): 32 x 2 x 4 = 256 triples
     assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 512
     assert lib.l20_pd_default_split_size(1, 8, 16384, 256) == 512
+    assert lib.l20_pd_default_split_size(16, 2, 8192, 256) == 1024  # 512 triples at 512, 256 at 1024
     assert lib.l20_pd_default_split_size(32, 2, 2048, 512) != 512  # 256 triples: half of 512 CUs
     assert lib.l20_pd_default_split_size(32, 2, 2048, 128) != 512  # 256 triples on 128 CUs
     assert lib.l20_pd_default_split_size(4, 2, 512, 256) == 64
@@ -259,6 +262,13 @@ def test_split_mode_rule(monkeypatch):
     assert cabi.launch_path(a) == 0
     a.batch = 17  # 272 triples
     assert cabi.launch_path(a) == 0
+    a.batch = 8
+    _with_split(a, 1024)  # 8 x 4 x 2 = 64 triples: a quarter of the CUs
+    assert cabi.launch_path(a) == 0
+    a.max_seq_len, a.bt_stride_row, a.bt_max_pages = 8192, 512, 512
+    _with_split(a, 1024)  # 8 x 4 x 8 = 256 triples
+    assert cabi.launch_path(a) == 2
+    a.max_seq_len, a.bt_stride_row, a.bt_max_pages = 2048, 128, 128
     a.batch = 16
     _with_split(a, 256)  # other splits: the persistent kernel
     assert cabi.launch_path(a) == 0

@@ -11,7 +11,8 @@ one split writes its output rows directly.
   256, 512 and 1024 tokens: 1, 2 and 4 fp8 blocks per wave), over fp32, fp16
   and bf16 workspaces: output and LSE against the oracle, through the C ABI.
 * The library's own choice at config 2 (its default split of 512 takes the
-  mode) at full size, against the oracle.
+  mode) at full size, and at 1024-token splits (8 x 8192 tokens, 4 KV heads),
+  against the oracle.
 * Graph capture: replays bitwise equal to the eager call; prior workspace
   contents (NaN) change nothing.
 """
@@ -199,3 +200,18 @@ def test_split_mode_graph_replays_and_prior_contents(monkeypatch):
         cabi.split_out(args, torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         assert torch.equal(out, eager[0]) and torch.equal(lse, eager[1])
+
+
+def test_library_takes_the_split_mode_at_1024_token_splits(monkeypatch):
+    """8 x 8192 tokens, 28 query / 4 KV heads: 512 triples at 512-token splits,
+    256 at 1024, so the library's split is 1024 and the partial stage the split
+    mode (four fp8 blocks per wave); against the oracle."""
+    import l20_pd_cabi as cabi
+
+    monkeypatch.delenv("L20_PD_FUSED_SPLIT", raising=False)
+    inp = H.make_synthetic(8, 28, 4, 128, [8192, 8000, 7001, 8192, 6500, 8192, 7777, 8100], seed=23)
+    split = int(cabi.load().l20_pd_default_split_size(8, 4, inp["max_seq_len"], 0))
+    assert split == 1024
+    out, lse, path = _run(inp, split, torch.float16)
+    assert path == 2
+    H.compare(out, lse, *H.run_oracle(inp))
