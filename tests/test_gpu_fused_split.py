@@ -215,3 +215,21 @@ def test_library_takes_the_split_mode_at_1024_token_splits(monkeypatch):
     out, lse, path = _run(inp, split, torch.float16)
     assert path == 2
     H.compare(out, lse, *H.run_oracle(inp))
+
+
+def test_noalloc_entry_in_split_mode(monkeypatch):
+    """The allocation-free entry point runs the same rule: split-mode calls
+    (the library's scratch array as the workspace) match the caller-workspace
+    entry point bitwise, on a large call and then a smaller one."""
+    import l20_pd_cabi as cabi
+    from test_zz_no_alloc import run_noalloc
+
+    monkeypatch.setenv("L20_PD_FUSED_SPLIT", "1")
+    big = H.make_synthetic(8, 28, 4, 128, [5000, 17, 1025, 3000, 512, 4097, 64, 2048], seed=81)
+    small = H.make_synthetic(3, 16, 2, 128, [1700, 100, 1033], seed=82)
+    for inp, split in ((big, 1024), (small, 512)):
+        print("noalloc split-mode case", inp["query"].shape, split, flush=True)
+        want = H.run_op(inp, split, via="cabi")
+        got = run_noalloc(inp, split)
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+        H.compare(*got, *H.run_oracle(inp))
