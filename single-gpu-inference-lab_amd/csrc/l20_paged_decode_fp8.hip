@@ -1799,8 +1799,6 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   // (whole sequences: the host launches this kernel only when l_cap <=
   // kFusedMaxTokens; splits: the host checks S / kFusedWaves <= 1024 and
   // the block size divides it)
-  // page ids of the wave's range: lane t -> tile t (-1 past the range, past
-  // the page list, and for an id outside the cache)
   const int32_t *row = p.indptr ? p.bt + uniform_ld(p.indptr, b) : p.bt + (int64_t)b * p.bt_srow;
   const int npages = p.indptr ? uniform_ld(p.indptr, b + 1) - uniform_ld(p.indptr, b) : p.bt_pages;
   auto tile_id = [&](int T) {
@@ -1825,6 +1823,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   const int uEnd = min(start + S, sEnd);
   const int tiles = max(0, (uEnd - start + kPage - 1) / kPage);
   const int nU = KT != 1 ? (tiles + 1) >> 1 : tiles;
+  // page ids of the wave's range: lane t -> tile t (-1 past the range, past
+  // the page list, and for an id outside the cache)
   int pid = -1;
   if (lane < tiles && lane < npages * p.page_mult - start / kPage) pid = tile_id(start / kPage + lane);
   qvec8 qop[NQT][U::NS];
