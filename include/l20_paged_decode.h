@@ -216,7 +216,7 @@ int32_t l20_pd_set_spin_limit(uint32_t polls);
  * The single launch is taken for G x q_len <= 32 (tree masks included),
  * batch x num_kv_heads <= the CU count and at most 1024 (fp8 caches) or 640
  * (16-bit caches) tokens per sequence within reach of the call; the split
- * mode for 512- or 1024-token splits whose batch x num_kv_heads x splits
+ * mode for 256-, 512- or 1024-token splits whose batch x num_kv_heads x splits
  * triples fill more than half the CUs without exceeding them. */
 int32_t l20_pd_single_launch(const l20_pd_fp8_args *args);
 

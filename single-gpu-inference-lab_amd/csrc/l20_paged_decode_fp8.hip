@@ -2580,10 +2580,10 @@ bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nq
 // folded in LDS, the split's partial written for the merge) rather than the
 // persistent partial kernel: each wave's share of a split (S / 8 tokens) must
 // be whole blocks and fit one page-id register, and by the size rule the
-// split is 512 or 1024 tokens (two or four fp8 blocks per wave, two in
-// flight) and the (split, sequence, KV head) triples fill more than half the
-// CUs without exceeding them: one 8-wave workgroup per CU, every wave's
-// blocks streaming at once.
+// split is 256, 512 or 1024 tokens (one, two or four fp8 blocks per wave, at
+// most two in flight) and the (split, sequence, KV head) triples fill more
+// than half the CUs without exceeding them: one 8-wave workgroup per CU,
+// every wave's blocks streaming at once.
 // Measured in one process against the persistent kernel at the library's
 // split, 33.5 MB of KV per call, µs per call: 32 x 2048 tokens, 2 KV heads
 // (config 2) 13.5-13.9 against 14.7; 16 x 2048, 4 KV heads 14.1 against
@@ -2597,7 +2597,10 @@ bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nq
 // against 23.4; 8 x 8192, 4 KV heads 18.6 against 23.5; 64 x 2048, 2 KV heads
 // 18.5 against 19.2.  Outside the rule it loses: 1024 triples at 1024 tokens
 // (128 x 1536, 4 KV heads) 50.2 against 41.6, (2 x 65536, 8 KV heads) 62.1
-// against 57.0.  L20_PD_FUSED_SPLIT=0/1 overrides the size rule.
+// against 57.0.  At 256-token splits, 16.8 MB per call: 16 x 2048 tokens, 2 KV
+// heads 10.9 against 12.9 (split 64); 8 x 2048, 4 KV heads 11.0 against 14.9;
+// 4 x 2048, 8 KV heads 10.8 against 14.6; 2 x 4096, 8 KV heads 11.0 against
+// 14.7.  L20_PD_FUSED_SPLIT=0/1 overrides the size rule.
 bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
   if (nqt > 2 || pp.num_splits < 2) return false;
   const int blk = kv16 ? 16 : 32;
@@ -2609,7 +2612,7 @@ bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, 
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  return (a.split_size == 512 || a.split_size == 1024) && 2 * triples > cus && triples <= cus;
+  return (a.split_size == 256 || a.split_size == 512 || a.split_size == 1024) && 2 * triples > cus && triples <= cus;
 }
 
 template <typename QT, int D, int WPP>
@@ -3003,13 +3006,13 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
   // contexts (fewer partials to merge), and at least ~8 splits per sequence
   // for short contexts, where the launch is latency-bound.
   if (max_seq_len > 32768) return 1024;
-  // Beyond the single launch's reach (1024 tokens), a batch whose 512-token
-  // (else 1024-token) (split, sequence, KV head) triples fill more than half
-  // the CUs without exceeding them runs the single-launch kernel's split mode
-  // at that split.
+  // Beyond the single launch's reach (1024 tokens), a batch whose 256-, 512-
+  // or 1024-token (split, sequence, KV head) triples (the first that does)
+  // fill more than half the CUs without exceeding them runs the single-launch
+  // kernel's split mode at that split.
   if (max_seq_len > 1024) {
     const int64_t cus = cu_count > 0 ? cu_count : 256;
-    for (const int32_t sp : {512, 1024}) {
+    for (const int32_t sp : {256, 512, 1024}) {
       const int64_t triples = (int64_t)batch * (num_kv_heads > 0 ? num_kv_heads : 1) * l20_pd_num_splits(max_seq_len, sp);
       if (2 * triples > cus && triples <= cus) return sp;
     }

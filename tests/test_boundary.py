@@ -65,6 +65,7 @@ def test_num_splits_and_default_split_size():
     assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 512
     assert lib.l20_pd_default_split_size(1, 8, 16384, 256) == 512
     assert lib.l20_pd_default_split_size(16, 2, 8192, 256) == 1024  # 512 triples at 512, 256 at 1024
+    assert lib.l20_pd_default_split_size(16, 2, 2048, 256) == 256  # 256 triples at 256
     assert lib.l20_pd_default_split_size(32, 2, 2048, 512) != 512  # 256 triples: half of 512 CUs
     assert lib.l20_pd_default_split_size(32, 2, 2048, 128) != 512  # 256 triples on 128 CUs
     assert lib.l20_pd_default_split_size(4, 2, 512, 256) == 64
@@ -270,7 +271,11 @@ def test_split_mode_rule(monkeypatch):
     assert cabi.launch_path(a) == 2
     a.max_seq_len, a.bt_stride_row, a.bt_max_pages = 2048, 128, 128
     a.batch = 16
-    _with_split(a, 256)  # other splits: the persistent kernel
+    _with_split(a, 256)  # 16 x 4 x 8 = 512 triples: two rounds
+    assert cabi.launch_path(a) == 0
+    a.batch = 8
+    assert cabi.launch_path(a) == 2  # 256 triples at 256-token splits (one block per wave)
+    a.batch = 16
     assert cabi.launch_path(a) == 0
     monkeypatch.setenv("L20_PD_FUSED_SPLIT", "1")
     assert cabi.launch_path(a) == 2

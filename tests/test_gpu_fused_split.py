@@ -11,8 +11,8 @@ one split writes its output rows directly.
   256, 512 and 1024 tokens: 1, 2 and 4 fp8 blocks per wave), over fp32, fp16
   and bf16 workspaces: output and LSE against the oracle, through the C ABI.
 * The library's own choice at config 2 (its default split of 512 takes the
-  mode) at full size, and at 1024-token splits (8 x 8192 tokens, 4 KV heads),
-  against the oracle.
+  mode) at full size, and at 256- and 1024-token splits (8 x 2048 and 8 x 8192
+  tokens, 4 KV heads), against the oracle.
 * Graph capture: replays bitwise equal to the eager call; prior workspace
   contents (NaN) change nothing.
 """
@@ -233,3 +233,17 @@ def test_noalloc_entry_in_split_mode(monkeypatch):
         got = run_noalloc(inp, split)
         assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
         H.compare(*got, *H.run_oracle(inp))
+
+
+def test_library_takes_the_split_mode_at_256_token_splits(monkeypatch):
+    """8 x 2048 tokens, 28 query / 4 KV heads: 256 triples at 256-token splits
+    (one fp8 block per wave), the library's split; against the oracle."""
+    import l20_pd_cabi as cabi
+
+    monkeypatch.delenv("L20_PD_FUSED_SPLIT", raising=False)
+    inp = H.make_synthetic(8, 28, 4, 128, [2048, 2000, 1100, 2048, 1500, 2048, 1777, 2040], per_head=True, seed=29)
+    split = int(cabi.load().l20_pd_default_split_size(8, 4, inp["max_seq_len"], 0))
+    assert split == 256
+    out, lse, path = _run(inp, split, torch.float16)
+    assert path == 2
+    H.compare(out, lse, *H.run_oracle(inp))
