@@ -4,7 +4,8 @@ Each case draws a batch, head layout, head_dim, q_len, cache dtype (e4m3fn, fp16
 bf16; a second range of seeds uses e5m2 caches), scale
 kind, ragged lengths (empty sequences and page-boundary lengths included),
 split size, workspace dtype and (fp8, q_len > 1) arbitrary tree-mask words
-from a fixed seed, runs the op, and compares
+from a fixed seed, runs the op (a third seed range with the single-launch
+kernel's split mode forced), and compares
 with the CPU oracle at the tolerances in ``pd_helpers``.  Sizes stay small so
 that the oracle finishes each case in well under a second.
 """
@@ -87,5 +88,20 @@ def test_random_shape(case):
 def test_random_shape_e5m2(case):
     """Another seed range with OCP e5m2 caches (the draws' other fields as above)."""
     c = dict(draw(case, seed_base=5000), cache="e5m2")
+    print(case, c, flush=True)
+    run_case(c)
+
+
+N_SPLIT_MODE = 48
+
+
+@pytest.mark.parametrize("case", range(N_SPLIT_MODE))
+def test_random_shape_split_mode(case, monkeypatch):
+    """A third seed range with the single-launch kernel's split mode forced
+    (L20_PD_FUSED_SPLIT=1) at the splits it accepts (256, 512, 1024 tokens);
+    calls with one split slot still run the persistent kernel."""
+    monkeypatch.setenv("L20_PD_FUSED_SPLIT", "1")
+    c = draw(case, seed_base=9000)
+    c["split"] = int(np.random.default_rng(9000 + case).choice([256, 256, 512, 1024]))
     print(case, c, flush=True)
     run_case(c)
