@@ -2575,15 +2575,21 @@ bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nq
   return (int64_t)a.batch * a.num_kv_heads <= cus && pp.l_cap <= (kv16 ? 640 : 1024);
 }
 
+// The split mode's size rule (see fused_split_fits).
+bool split_mode_fills(int split, int64_t triples, int64_t cus) {
+  if (split != 256 && split != 512 && split != 1024) return false;
+  return triples <= cus && (split == 1024 ? 2 * triples > cus : 2 * triples >= cus);
+}
+
 // Whether the partial stage of a split call runs as the single-launch kernel's
 // split mode (one workgroup per (split, sequence, KV head), its waves' states
 // folded in LDS, the split's partial written for the merge) rather than the
 // persistent partial kernel: each wave's share of a split (S / 8 tokens) must
 // be whole blocks and fit one page-id register, and by the size rule the
 // split is 256, 512 or 1024 tokens (one, two or four fp8 blocks per wave, at
-// most two in flight) and the (split, sequence, KV head) triples fill more
-// than half the CUs without exceeding them: one 8-wave workgroup per CU,
-// every wave's blocks streaming at once.
+// most two in flight) and the (split, sequence, KV head) triples fill at
+// least half the CUs (more than half at 1024) without exceeding them: one
+// 8-wave workgroup per CU, every wave's blocks streaming at once.
 // Measured in one process against the persistent kernel at the library's
 // split, 33.5 MB of KV per call, µs per call: 32 x 2048 tokens, 2 KV heads
 // (config 2) 13.5-13.9 against 14.7; 16 x 2048, 4 KV heads 14.1 against
@@ -2600,7 +2606,11 @@ bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nq
 // against 57.0.  At 256-token splits, 16.8 MB per call: 16 x 2048 tokens, 2 KV
 // heads 10.9 against 12.9 (split 64); 8 x 2048, 4 KV heads 11.0 against 14.9;
 // 4 x 2048, 8 KV heads 10.8 against 14.6; 2 x 4096, 8 KV heads 11.0 against
-// 14.7.  L20_PD_FUSED_SPLIT=0/1 overrides the size rule.
+// 14.7.  At half the CUs (128 triples): 8 x 2048 tokens, 2 KV heads, 256-token
+// splits 10.5 against 12.1 (split 64); 2 x 2048, 8 KV heads 10.1 against 14.2;
+// 16 x 4096, 2 KV heads, 512-token splits 14.1 against 14.9; but config 2 at
+// 1024-token splits 15.3 against 14.7.  L20_PD_FUSED_SPLIT=0/1 overrides the
+// size rule.
 bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
   if (nqt > 2 || pp.num_splits < 2) return false;
   const int blk = kv16 ? 16 : 32;
@@ -2612,7 +2622,7 @@ bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, 
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  return (a.split_size == 256 || a.split_size == 512 || a.split_size == 1024) && 2 * triples > cus && triples <= cus;
+  return split_mode_fills(a.split_size, triples, cus);
 }
 
 template <typename QT, int D, int WPP>
@@ -3008,13 +3018,13 @@ int32_t l20_pd_default_split_size(int32_t batch, int32_t num_kv_heads, int32_t m
   if (max_seq_len > 32768) return 1024;
   // Beyond the single launch's reach (1024 tokens), a batch whose 256-, 512-
   // or 1024-token (split, sequence, KV head) triples (the first that does)
-  // fill more than half the CUs without exceeding them runs the single-launch
+  // fill the CUs once by the split mode's rule runs the single-launch
   // kernel's split mode at that split.
   if (max_seq_len > 1024) {
     const int64_t cus = cu_count > 0 ? cu_count : 256;
     for (const int32_t sp : {256, 512, 1024}) {
       const int64_t triples = (int64_t)batch * (num_kv_heads > 0 ? num_kv_heads : 1) * l20_pd_num_splits(max_seq_len, sp);
-      if (2 * triples > cus && triples <= cus) return sp;
+      if (split_mode_fills(sp, triples, cus)) return sp;
     }
   }
   int32_t s = 512;
