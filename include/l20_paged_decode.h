@@ -217,8 +217,8 @@ int32_t l20_pd_set_spin_limit(uint32_t polls);
  * batch x num_kv_heads <= the CU count and at most 1024 (fp8 caches) or 640
  * (16-bit caches) tokens per sequence within reach of the call; the split
  * mode for 256-, 512- or 1024-token splits whose batch x num_kv_heads x splits
- * triples fill at least half the CUs (more than half at 1024) without
- * exceeding them. */
+ * triples do not exceed the CUs and, at 512 (1024) tokens, fill at least (more
+ * than) half of them. */
 int32_t l20_pd_single_launch(const l20_pd_fp8_args *args);
 
 /* Sets every work-queue counter of the current device to `value` (after a

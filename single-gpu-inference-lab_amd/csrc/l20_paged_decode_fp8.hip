@@ -2575,10 +2575,14 @@ bool fused_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nq
   return (int64_t)a.batch * a.num_kv_heads <= cus && pp.l_cap <= (kv16 ? 640 : 1024);
 }
 
-// The split mode's size rule (see fused_split_fits).
+// The split mode's size rule (see fused_split_fits): every triple on a CU of
+// its own, and at 512 (1024) tokens at least (more than) half of the CUs
+// busy; at 256 tokens (one fp8 block per wave) any count.
 bool split_mode_fills(int split, int64_t triples, int64_t cus) {
-  if (split != 256 && split != 512 && split != 1024) return false;
-  return triples <= cus && (split == 1024 ? 2 * triples > cus : 2 * triples >= cus);
+  if (triples > cus) return false;
+  if (split == 256) return true;
+  if (split == 512) return 2 * triples >= cus;
+  return split == 1024 && 2 * triples > cus;
 }
 
 // Whether the partial stage of a split call runs as the single-launch kernel's
@@ -2587,9 +2591,9 @@ bool split_mode_fills(int split, int64_t triples, int64_t cus) {
 // persistent partial kernel: each wave's share of a split (S / 8 tokens) must
 // be whole blocks and fit one page-id register, and by the size rule the
 // split is 256, 512 or 1024 tokens (one, two or four fp8 blocks per wave, at
-// most two in flight) and the (split, sequence, KV head) triples fill at
-// least half the CUs (more than half at 1024) without exceeding them: one
-// 8-wave workgroup per CU, every wave's blocks streaming at once.
+// most two in flight) and the (split, sequence, KV head) triples do not
+// exceed the CUs and, at 512 (1024) tokens, fill at least (more than) half of
+// them: one 8-wave workgroup per CU, every wave's blocks streaming at once.
 // Measured in one process against the persistent kernel at the library's
 // split, 33.5 MB of KV per call, µs per call: 32 x 2048 tokens, 2 KV heads
 // (config 2) 13.5-13.9 against 14.7; 16 x 2048, 4 KV heads 14.1 against
@@ -2609,8 +2613,13 @@ bool split_mode_fills(int split, int64_t triples, int64_t cus) {
 // 14.7.  At half the CUs (128 triples): 8 x 2048 tokens, 2 KV heads, 256-token
 // splits 10.5 against 12.1 (split 64); 2 x 2048, 8 KV heads 10.1 against 14.2;
 // 16 x 4096, 2 KV heads, 512-token splits 14.1 against 14.9; but config 2 at
-// 1024-token splits 15.3 against 14.7.  L20_PD_FUSED_SPLIT=0/1 overrides the
-// size rule.
+// 1024-token splits 15.3 against 14.7.  At 256-token splits with few triples:
+// 1 x 1100 tokens, 2 KV heads (10 triples) 9.6 against 11.7 (split 64);
+// 3 x 2048, 2 KV heads (48) 10.3 against 11.9; 1 x 4096, 2 KV heads (32) 10.2
+// against 12.0; 1 x 2048, 8 KV heads (64) 9.9 against 14.1; verification (q_len
+// 4, two query tiles) 2 x 1500, 16 / 2 heads 13.4 against 12.9 (split 64;
+// 19.1 at 256), 4 x 2048, 32 / 4 heads 14.0 against 16.1, 1 x 4096, 64 / 8
+// heads 14.3 against 19.6.  L20_PD_FUSED_SPLIT=0/1 overrides the size rule.
 bool fused_split_fits(const l20_pd_fp8_args &a, const l20pd::PartialParams &pp, int nqt, bool kv16) {
   if (nqt > 2 || pp.num_splits < 2) return false;
   const int blk = kv16 ? 16 : 32;

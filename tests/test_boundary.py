@@ -60,14 +60,15 @@ def test_num_splits_and_default_split_size():
     assert lib.l20_pd_default_split_size(64, 2, 2048, 512) == 512  # 512 triples on 512 CUs
     assert lib.l20_pd_default_split_size(128, 2, 2048, 256) == 256  # 512 triples at 1024: the persistent rules
     # the first of 256, 512 and 1024 whose (split, sequence, KV head) triples
-    # of a batch beyond 1024 tokens fill at least half the CUs (more than half
-    # at 1024) without exceeding them (the single-launch kernel's split mode):
-    # 32 x 2 x 4 = 256 triples at 512
+    # of a batch beyond 1024 tokens fit the CUs (and at 512 / 1024 tokens fill
+    # at least / more than half of them: the single-launch kernel's split
+    # mode): 32 x 2 x 4 = 256 triples at 512
     assert lib.l20_pd_default_split_size(32, 2, 2048, 256) == 512
     assert lib.l20_pd_default_split_size(1, 8, 16384, 256) == 512
     assert lib.l20_pd_default_split_size(16, 2, 8192, 256) == 1024  # 512 triples at 512, 256 at 1024
     assert lib.l20_pd_default_split_size(16, 2, 2048, 256) == 256  # 256 triples at 256
-    assert lib.l20_pd_default_split_size(8, 2, 2048, 256) == 256  # 128 triples at 256: half the CUs
+    assert lib.l20_pd_default_split_size(8, 2, 2048, 256) == 256  # 128 triples at 256
+    assert lib.l20_pd_default_split_size(1, 2, 1100, 256) == 256  # 10 triples at 256: any count
     assert lib.l20_pd_default_split_size(16, 2, 4096, 256) == 512  # 512 triples at 256, 128 at 512
     assert lib.l20_pd_default_split_size(32, 2, 2048, 512) != 512  # 256 triples: half of 512 CUs
     assert lib.l20_pd_default_split_size(32, 2, 2048, 128) != 512  # 256 triples on 128 CUs
@@ -251,10 +252,10 @@ def _with_split(a, split):
 def test_split_mode_rule(monkeypatch):
     """l20_pd_single_launch returns 2 when the partial stage runs as the
     single-launch kernel's split mode (one workgroup per (split, sequence, KV
-    head), merge after): 256-, 512- or 1024-token splits whose triples fill at
-    least half the CUs (256 here, no GPU; more than half at 1024) without
-    exceeding them; L20_PD_FUSED_SPLIT=0/1 overrides the size rule, not the
-    shape conditions."""
+    head), merge after): 256-, 512- or 1024-token splits whose triples do not
+    exceed the CUs (256 here, no GPU) and, at 512 (1024) tokens, fill at least
+    (more than) half of them; L20_PD_FUSED_SPLIT=0/1 overrides the size rule,
+    not the shape conditions."""
     monkeypatch.delenv("L20_PD_FUSED", raising=False)
     monkeypatch.delenv("L20_PD_FUSED_SPLIT", raising=False)
     a = valid_args()  # 28 query / 4 KV heads
@@ -282,6 +283,8 @@ def test_split_mode_rule(monkeypatch):
     assert cabi.launch_path(a) == 0
     a.batch = 8
     assert cabi.launch_path(a) == 2  # 256 triples at 256-token splits (one block per wave)
+    a.batch = 1
+    assert cabi.launch_path(a) == 2  # 32 triples: any count at 256 tokens
     a.batch = 16
     assert cabi.launch_path(a) == 0
     monkeypatch.setenv("L20_PD_FUSED_SPLIT", "1")
