@@ -1772,7 +1772,7 @@ struct FoldSlots {
 // verification as in the partial kernel.  The fold slots hold fp32 rows for
 // one tile and fp16 rows for two (fp32 would take 128 KB of LDS), the
 // precision of the 16-bit split workspaces.
-template <typename QT, int KT, int D, int NQT, bool TREE, int NBF>
+template <typename QT, int KT, int D, int NQT, bool TREE, int NBF, bool SPLIT>
 __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p) {
   typedef KvUnit<QT, KT, D, NQT, TREE, KT != 1 && D == 128 && (NBF == 1 || NQT == 1)> U;
   constexpr int kTok = U::kTok;
@@ -1788,17 +1788,25 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15;
   const int j = lane >> 4;
-  const int SS = p.fused_split;
+  // split mode as a separate instance: the whole-sequence launch keeps none of
+  // its arithmetic
+  const int SS = SPLIT ? p.fused_split : 0;
   const unsigned int pairs = (unsigned int)p.batch * (unsigned int)p.num_kv_heads;
   const int split = SS ? (int)(blockIdx.x / pairs) : 0;
   const int pair = (int)(blockIdx.x - (unsigned int)split * pairs);
-  const int b = pair / p.num_kv_heads;
+  const int b = (int)((unsigned int)pair / (unsigned int)p.num_kv_heads);
   const int kvh = pair - b * p.num_kv_heads;
   char *const kx = s_kx + (U::kKLines ? wave * U::kKxBytes : 0);
   const int q_len = p.q_len;
   // (whole sequences: the host launches this kernel only when l_cap <=
   // kFusedMaxTokens; splits: the host checks S / kFusedWaves <= 1024 and
-  // the block size divides it)
+  // the block size divides it).  The length loads first, with the kernel
+  // arguments: loaded after the page list's row, it took one more scalar
+  // round trip (config 1 5.80 -> 6.11 us per call, config 2 in the split mode
+  // 13.56 -> 13.81).
+  const int L = SS ? clamped_len(p, b) : min(clamped_len(p, b), kFusedMaxTokens);
+  const int n_b = SS ? splits_of_len(L, SS) : 1;
+  if (split >= n_b) return;  // the sequence has no such split (the whole workgroup)
   const int32_t *row = p.indptr ? p.bt + uniform_ld(p.indptr, b) : p.bt + (int64_t)b * p.bt_srow;
   const int npages = p.indptr ? uniform_ld(p.indptr, b + 1) - uniform_ld(p.indptr, b) : p.bt_pages;
   auto tile_id = [&](int T) {
@@ -1812,9 +1820,6 @@ __global__ __launch_bounds__(64 * kFusedWaves) void pd_fp8_fused(PartialParams p
     const int64_t v = (int64_t)e * m + (T - qq * m);
     return (e >= 0 && v < p.num_pages) ? (int)v : -1;
   };
-  const int L = SS ? clamped_len(p, b) : min(clamped_len(p, b), kFusedMaxTokens);
-  const int n_b = SS ? splits_of_len(L, SS) : 1;
-  if (split >= n_b) return;  // the sequence has no such split (the whole workgroup)
   const int sEnd = SS ? min((split + 1) * SS, L) : L;
   // (split mode: loading the span's page ids with the length instead, before
   // it is known, measured 0.15-0.2 us slower per call)
@@ -2532,8 +2537,13 @@ hipError_t launch_fused_tiles(const l20pd::PartialParams &pp, int head_dim, int 
   const dim3 grid((unsigned)((int64_t)batch * num_kv_heads * (pp.fused_split ? pp.num_splits : 1))),
       block(64 * l20pd::kFusedWaves);
   constexpr int NB = NQT == 1 ? kFusedNB : kFusedNB2;
-  if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, NQT, TREE, NB>), grid, block, 0, stream, pp);
-  else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, NQT, TREE, NB>), grid, block, 0, stream, pp);
+  if (pp.fused_split) {
+    if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, NQT, TREE, NB, true>), grid, block, 0, stream, pp);
+    else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, NQT, TREE, NB, true>), grid, block, 0, stream, pp);
+  } else {
+    if (head_dim == 128) hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 128, NQT, TREE, NB, false>), grid, block, 0, stream, pp);
+    else hipLaunchKernelGGL((l20pd::pd_fp8_fused<QT, KT, 64, NQT, TREE, NB, false>), grid, block, 0, stream, pp);
+  }
   return hipGetLastError();
 }
 template <typename QT, int KT>
